@@ -1,0 +1,167 @@
+"""Headline benchmark: fused Chronos-2 fp32 time attention at L=513, 12x64 heads, on one MI355X.
+
+One step is one launch of jc_c2_time_attention over the whole config-1 batch (B=256 series,
+L=513, 12 heads x 64; RoPE at load; left padding U{0..256} masked), inputs resident in HBM. The
+value is mask-aware TFLOP/s: sum over (series, head, query) of 4*dh*|live keys| per step, divided
+by the step time. The roofline object prices the kernel's average launch time (HIP events on the
+launch stream) against the fp32 MFMA peak; the CPU baseline is the C oracle (a restatement of the
+reference's CPU engine) timed on a bounded sample of the same workload on this host's cores.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+PEAK_FP32_TFLOPS = 157.3
+PEAK_HBM_GBS = 8000.0
+METRIC = "fused attention TFLOP/s (% MFMA peak) at L=513, 12x64 heads; forecast series/sec"
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def traffic_from_profile(name: str):
+    """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, scaled by a
+    known-size copy), committed as profiles/<name>.traffic.json; None when not measured."""
+    p = ROOT / "profiles" / f"{name}.traffic.json"
+    if not p.exists():
+        return None
+    try:
+        return json.loads(p.read_text()).get("bytes_per_launch")
+    except Exception:
+        return None
+
+
+def cpu_baseline(case, sample_rows: int, threads: int):
+    """Times the oracle (C restatement of CpuChronos2.timeAttention) on the first sample_rows rows."""
+    import numpy as np
+
+    sys.path.insert(0, str(ROOT))
+    from oracle import oracle
+
+    rows, n, heads, dh, inner = sample_rows, case.n, case.heads, case.dh, case.inner
+    qkv = case.qkv[: rows * n].float().cpu().numpy()
+    live = case.live[: rows * n].cpu().numpy().astype(np.int32)
+    oracle.lib()
+    t0 = time.perf_counter()
+    oracle.c2_time_attention(qkv, live, rows, n, heads, dh, inner, threads=threads)
+    dt = time.perf_counter() - t0
+    flops = 4.0 * dh * heads * n * float(live.sum())
+    return {
+        "value": round(flops / dt / 1e12, 6),
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{rows} of {case.rows} series of config 1 (L={n}, {heads}x{dh}), mask-aware flops, "
+                  f"{dt:.2f} s, double accumulation",
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-rows", type=int, default=256)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path (each series and each "
+              "group is independent; see DESIGN.md for how the path would shard)", file=sys.stderr)
+        return 2
+
+    import torch
+
+    import jitcast_amd
+    from jitcast_amd import chronos2, synthetic
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    log("generating config 1 inputs in HBM")
+    case = synthetic.c2_time_config1(device="cuda")
+    out = torch.empty(case.rows * case.n, case.inner, dtype=torch.float32, device=dev)
+    flops = case.mask_aware_flops()
+    dense = case.dense_flops()
+
+    def step():
+        chronos2.time_attention(case.qkv, out, case.live, case.rows, case.n, case.heads, case.dh, case.inner,
+                                case.table)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    log(f"warmup {args.warmup} done; timing {args.steps} steps")
+    stream = torch.cuda.current_stream()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for a, b in ev:
+        a.record(stream)
+        step()
+        b.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    launch_ms = sum(a.elapsed_time(b) for a, b in ev) / len(ev)
+    ms_per_step = wall * 1e3 / args.steps
+    value = flops / (ms_per_step * 1e-3) / 1e12
+    achieved = flops / (launch_ms * 1e-3) / 1e12
+    log(f"{ms_per_step:.4f} ms/step, kernel {launch_ms:.4f} ms, {achieved:.1f} TFLOP/s mask-aware, "
+        f"{dense / (launch_ms * 1e-3) / 1e12:.1f} dense")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        threads = os.cpu_count() or 1
+        try:
+            threads = min(threads, int(os.environ.get("OMP_NUM_THREADS", threads)))
+        except ValueError:
+            pass
+        log(f"cpu baseline on {args.cpu_rows} rows with {threads} threads")
+        cpu = cpu_baseline(case, args.cpu_rows, threads)
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (SplitMix64/Box-Muller seed 0: x~N(0,1), Wqkv~N(0,0.02), qkv=x Wqkv^T)",
+        "config": {
+            "workload": "config 1: isolated fp32 Chronos-2 time self-attention, RoPE at load, left padding "
+                        "U{0..256} masked",
+            "series": case.rows, "tokens": case.n, "heads": case.heads, "head_dim": case.dh,
+            "d_model": case.inner, "flops_per_step_mask_aware": flops, "flops_per_step_dense": dense,
+            "pct_of_fp32_mfma_peak": round(100 * value / PEAK_FP32_TFLOPS, 2),
+            "dense_tflops": round(dense / (ms_per_step * 1e-3) / 1e12, 3),
+        },
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(achieved, 3),
+            "peak": PEAK_FP32_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_FP32_TFLOPS, 4),
+            "traffic": traffic_from_profile("c2_time_attention_f32_config1"),
+            "kernel": "c2_time_attention_f32<64>",
+            "launch_ms": round(launch_ms, 5),
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

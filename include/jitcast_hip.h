@@ -1,0 +1,117 @@
+/*
+ * libjitcast_hip — C ABI of the MI355X (gfx950) encoder self-attention path.
+ *
+ * This is the drop-in boundary beside the reference's TornadoVM engines: a host (Java through
+ * Panama FFM downcalls, C++, or Python ctypes) owns device buffers allocated here, uploads the
+ * per-call inputs the reference's plans upload every run (tokens, RoPE table, live mask, group
+ * bounds; Chronos2Forward.java:248-249, 462-489), and calls one entry point per attention stage.
+ * Citations name the reference interface each entry point replaces; `J/` is
+ * src/main/java/ai/beestream/jitcast/ in the reference.
+ *
+ * Conventions (all entry points):
+ *   - return JC_OK (0) on success, a negative jc_status on error; jc_last_error() then holds a
+ *     thread-local message naming the entry point and the offending argument. Nothing throws or
+ *     aborts across this ABI.
+ *   - device pointers are caller-owned (jc_alloc or any hipMalloc'd memory); launches are
+ *     asynchronous on the context's stream; jc_sync waits.
+ *   - a jc_ctx is not thread-safe; callers serialise per engine, as the reference's
+ *     `synchronized PlanCache.run` does (J/tornado/PlanCache.java:70).
+ *   - activations are the reference's layout: qkv [rows*n, 3*inner], q|k|v heads-major per token
+ *     (h*dh + e); out [rows*n, inner]; masks int32 0/1.
+ */
+#ifndef JITCAST_HIP_H
+#define JITCAST_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum jc_status {
+    JC_OK = 0,
+    JC_EINVAL = -1,       /* a bad argument (shape, pointer, alignment, dtype) */
+    JC_EHIP = -2,         /* the HIP runtime reported an error */
+    JC_ENOMEM = -3,       /* device or host allocation failed */
+    JC_EUNSUPPORTED = -4, /* a valid request this build does not implement */
+    JC_ESTATE = -5        /* a call out of order (e.g. plan_end without plan_begin) */
+} jc_status;
+
+typedef enum jc_dtype {
+    JC_F32 = 0,  /* fp32 in and out, fp32 MFMA: the reference's FP32-exact default */
+    JC_BF16 = 1, /* bf16 qkv and out, bf16 MFMA with fp32 accumulation and fp32 softmax */
+    JC_F16 = 2   /* fp16 qkv and out (saturated to +-65504 as Kernels.java:42-46), fp32 accumulation */
+} jc_dtype;
+
+typedef struct jc_ctx jc_ctx;
+
+/* ---- runtime (replaces TornadoVM device selection and buffers: J/tornado/Devices.java:44-73) ---- */
+
+/* Makes `device` current and creates the context's stream (default priority). */
+int jc_init(int device, jc_ctx **ctx);
+/* Destroys the context (idempotent on NULL). */
+int jc_destroy(jc_ctx *ctx);
+/*
+ * Launches on an existing stream (e.g. a framework's current stream) instead of the context's
+ * own; NULL selects the device's default (null) stream. jc_stream() before the call returns the
+ * context's own stream, to restore it later.
+ */
+int jc_set_stream(jc_ctx *ctx, void *hip_stream);
+/* The stream launches go to. */
+void *jc_stream(jc_ctx *ctx);
+int jc_alloc(jc_ctx *ctx, size_t bytes, void **dptr);
+int jc_free(jc_ctx *ctx, void *dptr);
+int jc_memcpy_h2d(jc_ctx *ctx, void *dst, const void *src, size_t bytes);
+int jc_memcpy_d2h(jc_ctx *ctx, void *dst, const void *src, size_t bytes);
+int jc_memcpy_d2d(jc_ctx *ctx, void *dst, const void *src, size_t bytes);
+int jc_sync(jc_ctx *ctx);
+/* Compute units and the gfx architecture name of the context's device. */
+int jc_device_info(jc_ctx *ctx, int *compute_units, char *arch, size_t arch_len);
+/* The calling thread's last error message ("" if none). */
+const char *jc_last_error(void);
+/* 1 + the library's ABI revision. */
+int jc_version(void);
+
+/* ---- synthetic inputs (no reference counterpart: the benchmark's seeded generator) ---------------- */
+
+/*
+ * Fills device memory with the portable RNG: SplitMix64 output i of stream `stream_seed`
+ * (a case's tensor k uses seed*1000003 + k), 24-bit uniforms, Box-Muller normals in double rounded
+ * to float. Bit-compatible with jitcast_amd/rng.py up to the last-ulp rounding of the device's
+ * double log/cos/sin.
+ */
+int jc_fill_normal(jc_ctx *ctx, float *dptr, uint64_t count, uint64_t stream_seed, float mean, float stdv);
+int jc_fill_uniform(jc_ctx *ctx, float *dptr, uint64_t count, uint64_t stream_seed, float lo, float hi);
+
+/* ---- Chronos-2 time attention --------------------------------------------------------------- */
+
+/*
+ * The host-built RoPE table: table[p*dh + e] = cos((float)p * invFreq[e]) and
+ * table[p*dh + dh/2 + e] = sin(..), e < dh/2, cos/sin in double rounded to float, invFreq[i] =
+ * 1/(float)pow(theta, (float)(2i)/dh). Writes host memory [n*dh].
+ * Replaces Chronos2Forward.Plan.run's table fill (J/chronos2/tornado/Chronos2Forward.java:465-474)
+ * and CpuChronos2.inverseFrequencies (J/chronos2/cpu/CpuChronos2.java:102-111).
+ */
+int jc_c2_rope_table(int n, int dh, float theta, float *table_host);
+
+/*
+ * Fused RoPE + bidirectional time attention over the live keys of each row, unscaled scores;
+ * a query with no live key gets zeros.
+ * Replaces the pair Chronos2Kernels.rope(qkv, table, tokens, n, heads, dh, inner) and
+ * Chronos2Kernels.timeAttention(qkv, out, live, rows, n, heads, dh, inner)
+ * (J/chronos2/tornado/Chronos2Kernels.java:93-94, 130-131), oracle CpuChronos2.java:175-228.
+ *   qkv         device, [rows*n, 3*inner] of `dtype`; never written (RoPE is applied at load)
+ *   out         device, [rows*n, inner] of `dtype`
+ *   live        device, [rows*n] int32
+ *   rope_table  device, [n, dh] fp32 from jc_c2_rope_table, or NULL when q and k are already rotated
+ *   dh          a multiple of 8, at most 64 (the reference takes multiples of 16 up to 64,
+ *               Chronos2Forward.java:126-128); inner >= heads*dh, a multiple of 4; n <= 4096
+ */
+int jc_c2_time_attention(jc_ctx *ctx, const void *qkv, void *out, const int32_t *live, const float *rope_table,
+                         int rows, int n, int heads, int dh, int inner, int dtype);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

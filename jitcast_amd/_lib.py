@@ -1,0 +1,110 @@
+"""ctypes binding of libjitcast_hip (include/jitcast_hip.h).
+
+The library is the product: there is no fallback. If it is not built, loading raises
+LibraryMissing naming the build command.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "libjitcast_hip.so"
+HEADER = HERE.parent / "include" / "jitcast_hip.h"
+
+JC_OK, JC_EINVAL, JC_EHIP, JC_ENOMEM, JC_EUNSUPPORTED, JC_ESTATE = 0, -1, -2, -3, -4, -5
+JC_F32, JC_BF16, JC_F16 = 0, 1, 2
+
+
+class LibraryMissing(ImportError):
+    pass
+
+
+class JitcastError(RuntimeError):
+    """A non-zero jc_status; `code` is the status, the message is jc_last_error()."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(f"[{code}] {message}")
+        self.code = code
+
+
+class JitcastArgumentError(JitcastError, ValueError):
+    """JC_EINVAL: the reference throws IllegalArgumentException for these."""
+
+
+_c = ctypes
+_vp, _i, _f, _sz = _c.c_void_p, _c.c_int, _c.c_float, _c.c_size_t
+_i32p = _c.c_void_p  # device int32 pointers are passed as addresses
+
+# name -> (restype, argtypes); every function the header declares must be listed here
+SIGNATURES = {
+    "jc_init": (_i, [_i, _c.POINTER(_vp)]),
+    "jc_destroy": (_i, [_vp]),
+    "jc_set_stream": (_i, [_vp, _vp]),
+    "jc_stream": (_vp, [_vp]),
+    "jc_alloc": (_i, [_vp, _sz, _c.POINTER(_vp)]),
+    "jc_free": (_i, [_vp, _vp]),
+    "jc_memcpy_h2d": (_i, [_vp, _vp, _vp, _sz]),
+    "jc_memcpy_d2h": (_i, [_vp, _vp, _vp, _sz]),
+    "jc_memcpy_d2d": (_i, [_vp, _vp, _vp, _sz]),
+    "jc_sync": (_i, [_vp]),
+    "jc_device_info": (_i, [_vp, _c.POINTER(_i), _c.c_char_p, _sz]),
+    "jc_last_error": (_c.c_char_p, []),
+    "jc_version": (_i, []),
+    "jc_fill_normal": (_i, [_vp, _vp, _c.c_uint64, _c.c_uint64, _f, _f]),
+    "jc_fill_uniform": (_i, [_vp, _vp, _c.c_uint64, _c.c_uint64, _f, _f]),
+    "jc_c2_rope_table": (_i, [_i, _i, _f, _vp]),
+    "jc_c2_time_attention": (_i, [_vp, _vp, _vp, _i32p, _vp, _i, _i, _i, _i, _i, _i]),
+}
+
+_lib = None
+
+
+def header_symbols() -> list[str]:
+    """The function names include/jitcast_hip.h declares."""
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(jc_[a-z0-9_]+)\s*\(", text)))
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        path = Path(os.environ.get("JITCAST_HIP_LIB", LIB_PATH))
+        if not path.exists():
+            raise LibraryMissing(
+                f"{path} is not built; run `python -m jitcast_amd.build` (or __graft_entry__.build())")
+        # One HIP runtime per process: torch ships libamdhip64.so with SONAME libamdhip64.so.7. Loading
+        # torch first lets the dynamic loader resolve this library's libamdhip64.so.7 to that same
+        # copy, so device pointers and streams are shared. Without torch, /opt/rocm's runtime loads.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
+        handle = ctypes.CDLL(str(path))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = handle
+    return _lib
+
+
+def last_error() -> str:
+    msg = lib().jc_last_error()
+    return msg.decode() if msg else ""
+
+
+def check(rc: int) -> None:
+    if rc == JC_OK:
+        return
+    msg = last_error()
+    if rc == JC_EINVAL:
+        raise JitcastArgumentError(rc, msg)
+    raise JitcastError(rc, msg)
+
+
+def call(name: str, *args) -> None:
+    check(getattr(lib(), name)(*args))

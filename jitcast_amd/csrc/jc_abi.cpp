@@ -1,0 +1,235 @@
+// The C ABI of libjitcast_hip (include/jitcast_hip.h): argument checks, error capture and the
+// runtime helpers. Every entry point returns a jc_status and records a message; no exception or
+// abort crosses the boundary.
+#include "../../include/jitcast_hip.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <vector>
+
+#include "jc_kernels.hpp"
+
+struct jc_ctx {
+    int device;
+    hipStream_t own;     // created by jc_init
+    hipStream_t stream;  // where launches go (own, or a caller's)
+    int cus;
+    char arch[64];
+};
+
+namespace {
+
+thread_local char g_err[512];
+
+int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int hip_fail(const char* where, hipError_t e) {
+    return fail(JC_EHIP, "%s: %s (%d)", where, hipGetErrorString(e), (int)e);
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Makes the context's device current for this thread.
+int use(jc_ctx* ctx, const char* where) {
+    if (!ctx) return fail(JC_EINVAL, "%s: null context", where);
+    hipError_t e = hipSetDevice(ctx->device);
+    if (e != hipSuccess) return hip_fail(where, e);
+    return JC_OK;
+}
+
+size_t dtype_size(int dtype) { return dtype == JC_F32 ? 4 : 2; }
+
+}  // namespace
+
+extern "C" {
+
+const char* jc_last_error(void) { return g_err; }
+
+int jc_version(void) { return 1; }
+
+int jc_init(int device, jc_ctx** out) {
+    g_err[0] = 0;
+    if (!out) return fail(JC_EINVAL, "jc_init: null output pointer");
+    *out = nullptr;
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess) return hip_fail("jc_init: hipGetDeviceCount", e);
+    if (device < 0 || device >= count)
+        return fail(JC_EINVAL, "jc_init: device %d out of range (%d devices)", device, count);
+    e = hipSetDevice(device);
+    if (e != hipSuccess) return hip_fail("jc_init: hipSetDevice", e);
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, device);
+    if (e != hipSuccess) return hip_fail("jc_init: hipGetDeviceProperties", e);
+    jc_ctx* ctx = new (std::nothrow) jc_ctx();
+    if (!ctx) return fail(JC_ENOMEM, "jc_init: out of host memory");
+    ctx->device = device;
+    ctx->cus = prop.multiProcessorCount;
+    snprintf(ctx->arch, sizeof ctx->arch, "%s", prop.gcnArchName);
+    e = hipStreamCreateWithFlags(&ctx->own, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        delete ctx;
+        return hip_fail("jc_init: hipStreamCreate", e);
+    }
+    ctx->stream = ctx->own;
+    *out = ctx;
+    return JC_OK;
+}
+
+int jc_destroy(jc_ctx* ctx) {
+    if (!ctx) return JC_OK;
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    (void)hipStreamDestroy(ctx->own);
+    delete ctx;
+    return JC_OK;
+}
+
+int jc_set_stream(jc_ctx* ctx, void* stream) {
+    if (!ctx) return fail(JC_EINVAL, "jc_set_stream: null context");
+    ctx->stream = (hipStream_t)stream;  // NULL is the device's default (null) stream
+    return JC_OK;
+}
+
+void* jc_stream(jc_ctx* ctx) { return ctx ? (void*)ctx->stream : nullptr; }
+
+int jc_alloc(jc_ctx* ctx, size_t bytes, void** dptr) {
+    int rc = use(ctx, "jc_alloc");
+    if (rc) return rc;
+    if (!dptr) return fail(JC_EINVAL, "jc_alloc: null output pointer");
+    *dptr = nullptr;
+    if (bytes == 0) return JC_OK;
+    hipError_t e = hipMalloc(dptr, bytes);
+    if (e != hipSuccess) {
+        *dptr = nullptr;
+        return e == hipErrorOutOfMemory ? fail(JC_ENOMEM, "jc_alloc: out of device memory for %zu bytes", bytes)
+                                        : hip_fail("jc_alloc: hipMalloc", e);
+    }
+    return JC_OK;
+}
+
+int jc_free(jc_ctx* ctx, void* dptr) {
+    int rc = use(ctx, "jc_free");
+    if (rc) return rc;
+    if (!dptr) return JC_OK;
+    hipError_t e = hipFree(dptr);
+    return e == hipSuccess ? JC_OK : hip_fail("jc_free: hipFree", e);
+}
+
+static int copy(jc_ctx* ctx, void* dst, const void* src, size_t bytes, hipMemcpyKind kind, const char* where) {
+    int rc = use(ctx, where);
+    if (rc) return rc;
+    if (bytes == 0) return JC_OK;
+    if (!dst || !src) return fail(JC_EINVAL, "%s: null pointer", where);
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, kind, ctx->stream);
+    if (e != hipSuccess) return hip_fail(where, e);
+    if (kind != hipMemcpyDeviceToDevice) {
+        // host buffers are pageable: wait so the caller may reuse or read them on return
+        e = hipStreamSynchronize(ctx->stream);
+        if (e != hipSuccess) return hip_fail(where, e);
+    }
+    return JC_OK;
+}
+
+int jc_memcpy_h2d(jc_ctx* ctx, void* dst, const void* src, size_t bytes) {
+    return copy(ctx, dst, src, bytes, hipMemcpyHostToDevice, "jc_memcpy_h2d");
+}
+int jc_memcpy_d2h(jc_ctx* ctx, void* dst, const void* src, size_t bytes) {
+    return copy(ctx, dst, src, bytes, hipMemcpyDeviceToHost, "jc_memcpy_d2h");
+}
+int jc_memcpy_d2d(jc_ctx* ctx, void* dst, const void* src, size_t bytes) {
+    return copy(ctx, dst, src, bytes, hipMemcpyDeviceToDevice, "jc_memcpy_d2d");
+}
+
+int jc_sync(jc_ctx* ctx) {
+    int rc = use(ctx, "jc_sync");
+    if (rc) return rc;
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    return e == hipSuccess ? JC_OK : hip_fail("jc_sync", e);
+}
+
+int jc_device_info(jc_ctx* ctx, int* cus, char* arch, size_t arch_len) {
+    if (!ctx) return fail(JC_EINVAL, "jc_device_info: null context");
+    if (cus) *cus = ctx->cus;
+    if (arch && arch_len) snprintf(arch, arch_len, "%s", ctx->arch);
+    return JC_OK;
+}
+
+// ---- the portable RNG --------------------------------------------------------------------
+
+int jc_fill_normal(jc_ctx* ctx, float* dptr, uint64_t count, uint64_t stream_seed, float mean, float stdv) {
+    int rc = use(ctx, "jc_fill_normal");
+    if (rc) return rc;
+    if (count && !dptr) return fail(JC_EINVAL, "jc_fill_normal: null device pointer");
+    hipError_t e = jc::fill_normal_launch(dptr, count, stream_seed, mean, stdv, ctx->stream);
+    return e == hipSuccess ? JC_OK : hip_fail("jc_fill_normal", e);
+}
+
+int jc_fill_uniform(jc_ctx* ctx, float* dptr, uint64_t count, uint64_t stream_seed, float lo, float hi) {
+    int rc = use(ctx, "jc_fill_uniform");
+    if (rc) return rc;
+    if (count && !dptr) return fail(JC_EINVAL, "jc_fill_uniform: null device pointer");
+    hipError_t e = jc::fill_uniform_launch(dptr, count, stream_seed, lo, hi, ctx->stream);
+    return e == hipSuccess ? JC_OK : hip_fail("jc_fill_uniform", e);
+}
+
+// ---- Chronos-2 ------------------------------------------------------------------------------
+
+int jc_c2_rope_table(int n, int dh, float theta, float* table) {
+    if (n < 0 || dh < 2 || dh % 2 || !table || !(theta > 0.f))
+        return fail(JC_EINVAL, "jc_c2_rope_table: bad arguments (n=%d dh=%d theta=%g)", n, dh, (double)theta);
+    int half = dh / 2;
+    std::vector<float> inv(half);
+    for (int i = 0; i < half; i++) {
+        float ex = (float)(2 * i) / (float)dh;
+        inv[i] = 1.0f / (float)std::pow((double)theta, (double)ex);
+    }
+    for (int p = 0; p < n; p++) {
+        for (int e = 0; e < half; e++) {
+            float a = (float)p * inv[e];
+            table[(size_t)p * dh + e] = (float)std::cos((double)a);
+            table[(size_t)p * dh + half + e] = (float)std::sin((double)a);
+        }
+    }
+    return JC_OK;
+}
+
+int jc_c2_time_attention(jc_ctx* ctx, const void* qkv, void* out, const int32_t* live, const float* table, int rows,
+                         int n, int heads, int dh, int inner, int dtype) {
+    const char* W = "jc_c2_time_attention";
+    int rc = use(ctx, W);
+    if (rc) return rc;
+    if (rows < 0 || n < 0 || heads < 1) return fail(JC_EINVAL, "%s: bad shape rows=%d n=%d heads=%d", W, rows, n, heads);
+    if (dh < 8 || dh > 64 || dh % 8) return fail(JC_EINVAL, "%s: head width %d (need a multiple of 8, <= 64)", W, dh);
+    if (inner < heads * dh || inner % 4)
+        return fail(JC_EINVAL, "%s: inner %d (need >= heads*dh = %d and a multiple of 4)", W, inner, heads * dh);
+    if (n > jc::c2_time_attention_max_tokens())
+        return fail(JC_EINVAL, "%s: %d tokens per row (at most %d)", W, n, jc::c2_time_attention_max_tokens());
+    if (dtype != JC_F32 && dtype != JC_BF16 && dtype != JC_F16) return fail(JC_EINVAL, "%s: dtype %d", W, dtype);
+    if ((size_t)rows * n == 0) return JC_OK;
+    if (!qkv || !out || !live) return fail(JC_EINVAL, "%s: null device pointer", W);
+    if (!aligned16(qkv) || !aligned16(out) || (table && !aligned16(table)))
+        return fail(JC_EINVAL, "%s: qkv, out and rope_table must be 16-byte aligned", W);
+    if ((uint64_t)rows * heads * ((n + 127) / 128) > 0x7fffffffull) return fail(JC_EINVAL, "%s: grid too large", W);
+    hipError_t e;
+    if (dtype == JC_F32) {
+        e = jc::c2_time_attention_f32_launch((const float*)qkv, (float*)out, live, table, rows, n, heads, dh, inner,
+                                             ctx->stream);
+    } else {
+        return fail(JC_EUNSUPPORTED, "%s: dtype %d is not built yet", W, dtype);
+    }
+    return e == hipSuccess ? JC_OK : hip_fail(W, e);
+}
+
+}  // extern "C"

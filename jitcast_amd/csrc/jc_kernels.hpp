@@ -1,0 +1,19 @@
+// Internal launchers of the gfx950 kernels (host side). Each validates nothing: the C-ABI layer
+// (jc_abi.cpp) checks shapes, pointers and alignment before calling them.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace jc {
+
+hipError_t c2_time_attention_f32_launch(const float* qkv, float* out, const int32_t* live, const float* table,
+                                        int rows, int n, int heads, int dh, int inner, hipStream_t stream);
+int c2_time_attention_max_tokens();
+
+hipError_t fill_normal_launch(float* out, uint64_t count, uint64_t stream_seed, double mean, double stdv,
+                              hipStream_t stream);
+hipError_t fill_uniform_launch(float* out, uint64_t count, uint64_t stream_seed, double lo, double hi,
+                               hipStream_t stream);
+
+}  // namespace jc

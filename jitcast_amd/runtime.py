@@ -1,0 +1,78 @@
+"""The device context: one jc_ctx per device, launching on torch's current stream.
+
+PyTorch is plumbing here (device memory and streams); every computation on the attention path
+runs in libjitcast_hip.
+"""
+from __future__ import annotations
+
+import ctypes
+
+from . import _lib
+
+
+class HipContext:
+    """jc_init/jc_destroy around one device (J/tornado/Devices.java:44-73 picks the device)."""
+
+    def __init__(self, device: int = 0):
+        handle = ctypes.c_void_p()
+        _lib.call("jc_init", device, ctypes.byref(handle))
+        self.handle = handle
+        self.device = device
+
+    def bind_torch_stream(self) -> None:
+        """Launch on torch's current stream on this device, so launches order with torch work."""
+        import torch
+
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        _lib.call("jc_set_stream", self.handle, ctypes.c_void_p(stream))
+
+    def sync(self) -> None:
+        _lib.call("jc_sync", self.handle)
+
+    def device_info(self) -> tuple[int, str]:
+        cus = ctypes.c_int()
+        arch = ctypes.create_string_buffer(64)
+        _lib.call("jc_device_info", self.handle, ctypes.byref(cus), arch, 64)
+        return cus.value, arch.value.decode()
+
+    def close(self) -> None:
+        if self.handle:
+            _lib.lib().jc_destroy(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+_default: dict[int, HipContext] = {}
+
+
+def context(device: int = 0) -> HipContext:
+    """The process-wide context of a device, bound to torch's current stream on every call."""
+    ctx = _default.get(device)
+    if ctx is None:
+        ctx = _default[device] = HipContext(device)
+    ctx.bind_torch_stream()
+    return ctx
+
+
+def fill_normal(t, stream_seed: int, mean: float = 0.0, std: float = 1.0) -> None:
+    """Fills a float32 CUDA tensor in place with the portable RNG (jc_fill_normal)."""
+    ctx = context(t.device.index or 0)
+    _lib.call("jc_fill_normal", ctx.handle, ctypes.c_void_p(t.data_ptr()), t.numel(), stream_seed,
+              ctypes.c_float(mean), ctypes.c_float(std))
+
+
+def fill_uniform(t, stream_seed: int, lo: float = 0.0, hi: float = 1.0) -> None:
+    ctx = context(t.device.index or 0)
+    _lib.call("jc_fill_uniform", ctx.handle, ctypes.c_void_p(t.data_ptr()), t.numel(), stream_seed,
+              ctypes.c_float(lo), ctypes.c_float(hi))

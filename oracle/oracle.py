@@ -1,0 +1,170 @@
+"""ctypes wrapper of libjc_oracle.so, the C restatement of the reference's CPU attention stages.
+
+TEST INFRASTRUCTURE ONLY: the checker for libjitcast_hip. See jc_oracle.h for the reference
+file:line each function restates.
+"""
+from __future__ import annotations
+
+import ctypes
+import shutil
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB = HERE / "libjc_oracle.so"
+_lib = None
+
+
+def build() -> Path:
+    if shutil.which("make") is None:
+        raise RuntimeError("make is not available to build the oracle")
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    return LIB
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB.exists():
+            build()
+        _lib = ctypes.CDLL(str(LIB))
+        v, i, f, i64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_int64
+        sig = {
+            "jco_c2_inv_freq": (None, [i, f, v]),
+            "jco_c2_rope_table": (None, [i, i, f, v]),
+            "jco_c2_time_attention": (i, [v, v, v, i, i, i, i, i, f, i]),
+            "jco_c2_group_attention": (i, [v, v, v, v, i, i, i, i, i, i]),
+            "jco_c2_live": (None, [v, i, i, i, i, i, v]),
+            "jco_ts_inv_freq": (None, [i, i, f, v]),
+            "jco_ts_time_attention": (i, [v, v, v, v, v, i, i, i, i, i, i, i, i, f, i]),
+            "jco_ts_variate_attention": (i, [v, v, v, v, v, i, i, i, i, i, i, i, i]),
+            "jco_ts_gate": (None, [v, v, i64]),
+            "jco_linear": (None, [v, i, v, v, i, i, v, i]),
+            "jco_rms_norm": (None, [v, i, i, v, f, v]),
+            "jco_relu": (None, [v, i64]),
+            "jco_add": (None, [v, v, i64]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(_lib, name)
+            fn.restype = res
+            fn.argtypes = args
+    return _lib
+
+
+def _p(a: np.ndarray | None) -> ctypes.c_void_p:
+    return ctypes.c_void_p(0) if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _i32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.int32)
+
+
+def c2_inv_freq(dh: int, theta: float = 10000.0) -> np.ndarray:
+    out = np.empty(dh // 2, np.float32)
+    lib().jco_c2_inv_freq(dh, theta, _p(out))
+    return out
+
+
+def c2_rope_table(n: int, dh: int, theta: float = 10000.0) -> np.ndarray:
+    out = np.empty((n, dh), np.float32)
+    lib().jco_c2_rope_table(n, dh, theta, _p(out))
+    return out
+
+
+def c2_time_attention(qkv, live, rows, n, heads, dh, inner, theta=10000.0, threads=0) -> np.ndarray:
+    qkv, live = _f32(qkv), _i32(live)
+    out = np.empty((rows * n, inner), np.float32)
+    rc = lib().jco_c2_time_attention(_p(qkv), _p(out), _p(live), rows, n, heads, dh, inner, theta, threads)
+    if rc:
+        raise ValueError(f"jco_c2_time_attention: {rc}")
+    return out
+
+
+def c2_group_attention(qkv, live, group, rows, n, heads, dh, inner, threads=0) -> np.ndarray:
+    qkv, live, group = _f32(qkv), _i32(live), _i32(group)
+    out = np.empty((rows * n, inner), np.float32)
+    rc = lib().jco_c2_group_attention(_p(qkv), _p(out), _p(live), _p(group), rows, n, heads, dh, inner, threads)
+    if rc:
+        raise ValueError(f"jco_c2_group_attention: {rc}")
+    return out
+
+
+def c2_live(window, rows, nc, patch, reg, h) -> np.ndarray:
+    window = _f32(window)
+    out = np.empty((rows, nc + reg + h), np.int32)
+    lib().jco_c2_live(_p(window), rows, nc, patch, reg, h, _p(out))
+    return out
+
+
+def ts_inv_freq(dh: int, rope_dim: int, theta: float = 10000.0) -> np.ndarray:
+    out = np.empty(dh // 2, np.float32)
+    lib().jco_ts_inv_freq(dh, rope_dim, theta, _p(out))
+    return out
+
+
+def ts_time_attention(qkv, key_valid, known, pos, rows, enc, ll, n, heads, dh, d, rope_dim, theta=10000.0,
+                      threads=0) -> np.ndarray:
+    qkv, key_valid, known, pos = _f32(qkv), _i32(key_valid), _i32(known), _i32(pos)
+    out = np.empty((rows * n, d), np.float32)
+    rc = lib().jco_ts_time_attention(_p(qkv), _p(out), _p(key_valid), _p(known), _p(pos), rows, enc, ll, n, heads,
+                                     dh, d, rope_dim, theta, threads)
+    if rc:
+        raise ValueError(f"jco_ts_time_attention: {rc}")
+    return out
+
+
+def ts_variate_attention(qkv, key_valid, group, role, covariates, rows, enc, n, heads, dh, d, threads=0):
+    qkv, key_valid, group, role = _f32(qkv), _i32(key_valid), _i32(group), _i32(role)
+    out = np.empty((rows * n, d), np.float32)
+    rc = lib().jco_ts_variate_attention(_p(qkv), _p(out), _p(key_valid), _p(group), _p(role), int(covariates), rows,
+                                        enc, n, heads, dh, d, threads)
+    if rc:
+        raise ValueError(f"jco_ts_variate_attention: {rc}")
+    return out
+
+
+def ts_gate(att, g) -> np.ndarray:
+    att = _f32(att).copy()
+    g = _f32(g)
+    lib().jco_ts_gate(_p(att), _p(g), att.size)
+    return att
+
+
+def linear(x, w, b=None, threads=0) -> np.ndarray:
+    x, w = _f32(x), _f32(w)
+    rows, inn = x.shape
+    out_f = w.shape[0]
+    y = np.empty((rows, out_f), np.float32)
+    lib().jco_linear(_p(x), rows, _p(w), _p(None if b is None else _f32(b)), inn, out_f, _p(y), threads)
+    return y
+
+
+def rms_norm(x, w, eps) -> np.ndarray:
+    x = _f32(x)
+    rows, cols = x.shape
+    y = np.empty_like(x)
+    lib().jco_rms_norm(_p(x), rows, cols, _p(None if w is None else _f32(w)), eps, _p(y))
+    return y
+
+
+def rel_max_error(actual, expected) -> float:
+    """The reference's metric: max|a-e| / max(max|e|, 1e-6); a NaN mismatch is infinite
+    (T/chronos2/Chronos2Golden.java:218-234)."""
+    a = np.asarray(actual, dtype=np.float64)
+    e = np.asarray(expected, dtype=np.float64)
+    if a.shape != e.shape:
+        raise ValueError(f"shape {a.shape} vs {e.shape}")
+    if a.size == 0:
+        return 0.0
+    an, en = np.isnan(a), np.isnan(e)
+    if np.any(an != en):
+        return float("inf")
+    d = np.abs(np.where(an, 0, a) - np.where(en, 0, e))
+    scale = max(float(np.max(np.abs(np.where(en, 0, e)))), 1e-6)
+    return float(np.max(d)) / scale

@@ -1,0 +1,50 @@
+import os
+import sys
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (runs the HIP kernels through the C ABI)")
+    config.addinivalue_line("markers", "slow: a larger case (still minutes at most)")
+
+
+def pytest_collection_modifyitems(config, items):
+    # GPU tests first make sure the library is the HIP build, never a fallback
+    pass
+
+
+@pytest.fixture(scope="session")
+def oracle():
+    from oracle import oracle as o
+
+    o.lib()
+    return o
+
+
+@pytest.fixture(scope="session")
+def gpu():
+    """The device context; a GPU test fails (not skips) when the library or the GPU is missing."""
+    import torch
+
+    import jitcast_amd
+
+    assert torch.cuda.is_available(), "GPU test run without a visible GPU"
+    ctx = jitcast_amd.runtime.context(0)
+    cus, arch = ctx.device_info()
+    print(f"[gpu] {arch} with {cus} CUs", flush=True)
+    return ctx
+
+
+@pytest.fixture(scope="session", autouse=True)
+def _built_library():
+    """CPU tests load libjitcast_hip (symbols, host helpers); build it once if this tree has none."""
+    from jitcast_amd import build as b
+
+    if not b.LIB.exists():
+        b.build(verbose=False)

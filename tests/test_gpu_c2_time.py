@@ -1,0 +1,126 @@
+"""GPU parity of the fused Chronos-2 time attention against the C oracle (through the C ABI).
+
+Bar: max relative error (the reference's metric) <= 1e-4 for fp32.
+"""
+import numpy as np
+import pytest
+import torch
+
+from jitcast_amd import JitcastArgumentError, chronos2
+from tests import brute, cases
+
+pytestmark = pytest.mark.gpu
+TOL_F32 = 1e-4
+
+
+def _run(qkv, live, rows, n, heads, dh, inner, table=True, dtype=torch.float32):
+    dev = torch.device("cuda:0")
+    q = torch.from_numpy(qkv).to(dev).to(dtype)
+    out = torch.full((rows * n, inner), float("nan"), dtype=dtype, device=dev)
+    tab = torch.from_numpy(chronos2.rope_table(n, dh)).to(dev) if table else None
+    chronos2.time_attention(q, out, torch.from_numpy(np.ascontiguousarray(live.reshape(-1), np.int32)).to(dev),
+                            rows, n, heads, dh, inner, tab)
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy()
+
+
+CASES = [
+    # rows, n, heads, dh, inner, live kind
+    (2, 37, 2, 64, 128, "pad"),
+    (1, 1, 1, 64, 64, "all"),
+    (2, 2, 1, 64, 64, "all"),
+    (3, 31, 2, 64, 128, "random"),
+    (3, 32, 2, 64, 128, "random"),
+    (3, 33, 2, 64, 128, "pad"),
+    (2, 129, 3, 64, 192, "random"),
+    (2, 200, 2, 64, 136, "pad"),
+    (2, 77, 3, 32, 96, "pad"),
+    (2, 50, 2, 48, 100, "random"),
+    (2, 45, 4, 16, 64, "pad"),
+    (1, 600, 1, 64, 64, "pad"),
+]
+
+
+def _live(kind, seed, rows, n):
+    if kind == "pad":
+        return cases.left_pad_live(seed, rows, n, n // 2)
+    if kind == "random":
+        return cases.random_live(seed, rows, n, 0.5)
+    return np.ones((rows, n), np.int32)
+
+
+@pytest.mark.parametrize("rows,n,heads,dh,inner,kind", CASES)
+def test_fp32_matches_oracle(gpu, oracle, rows, n, heads, dh, inner, kind):
+    print(f"case rows={rows} n={n} heads={heads} dh={dh} inner={inner} {kind}", flush=True)
+    qkv = cases.qkv(23, rows * n, inner)
+    live = _live(kind, 23, rows, n)
+    got = _run(qkv, live, rows, n, heads, dh, inner)
+    exp = oracle.c2_time_attention(qkv, live, rows, n, heads, dh, inner)
+    # columns past heads*dh are not attention outputs: the kernel leaves them untouched
+    got, exp = got[:, : heads * dh], exp[:, : heads * dh]
+    assert np.isfinite(got).all()
+    assert oracle.rel_max_error(got, exp) <= TOL_F32
+
+
+def test_fp32_no_live_key_gives_zeros(gpu, oracle):
+    rows, n, heads, dh, inner = 3, 40, 2, 64, 128
+    qkv = cases.qkv(29, rows * n, inner)
+    live = cases.left_pad_live(29, rows, n, 10)
+    live[1] = 0
+    got = _run(qkv, live, rows, n, heads, dh, inner)
+    assert not np.any(got.reshape(rows, n, inner)[1])
+    exp = oracle.c2_time_attention(qkv, live, rows, n, heads, dh, inner)
+    assert oracle.rel_max_error(got, exp) <= TOL_F32
+
+
+def test_fp32_one_live_key_returns_its_value(gpu):
+    rows, n, heads, dh, inner = 2, 70, 2, 64, 128
+    qkv = cases.qkv(31, rows * n, inner)
+    live = np.zeros((rows, n), np.int32)
+    live[0, 3] = 1
+    live[1, 69] = 1
+    got = _run(qkv, live, rows, n, heads, dh, inner).reshape(rows, n, inner)
+    v = qkv.reshape(rows, n, 3 * inner)[:, :, 2 * inner:]
+    np.testing.assert_allclose(got[0], np.broadcast_to(v[0, 3], (n, inner)), rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(got[1], np.broadcast_to(v[1, 69], (n, inner)), rtol=1e-6, atol=1e-6)
+
+
+def test_fp32_without_table_is_plain_attention(gpu):
+    """rope_table NULL: qkv is taken as already rotated (the reference's separate rope task ran)."""
+    rows, n, heads, dh, inner = 2, 65, 2, 64, 128
+    qkv = cases.qkv(37, rows * n, inner)
+    live = cases.left_pad_live(37, rows, n, 30)
+    got = _run(qkv, live, rows, n, heads, dh, inner, table=False)
+    q, k, v = brute.split_qkv(qkv, rows, n, heads, dh, inner)
+    s = np.einsum("rqhe,rkhe->rhqk", q.astype(np.float64), k.astype(np.float64))
+    s = np.where(live[:, None, None, :] == 1, s, -np.inf)
+    p = np.exp(s - s.max(-1, keepdims=True))
+    o = np.einsum("rhqk,rkhe->rqhe", p / p.sum(-1, keepdims=True), v.astype(np.float64))
+    from oracle.oracle import rel_max_error
+    assert rel_max_error(got, o.reshape(rows * n, inner)) <= TOL_F32
+
+
+def test_config1_shape_subset_matches_oracle(gpu, oracle):
+    """The config-1 shape (L=513, 12x64, d 768, pads U{0..256}) on 12 series generated like the bench."""
+    from jitcast_amd import synthetic
+
+    case = synthetic.c2_time_config1(rows=12, device="cuda")
+    out = torch.empty(case.rows * case.n, case.inner, device="cuda")
+    chronos2.time_attention(case.qkv, out, case.live, case.rows, case.n, case.heads, case.dh, case.inner, case.table)
+    torch.cuda.synchronize()
+    exp = oracle.c2_time_attention(case.qkv.cpu().numpy(), case.live.cpu().numpy(), case.rows, case.n, case.heads,
+                                   case.dh, case.inner)
+    err = oracle.rel_max_error(out.cpu().numpy(), exp)
+    print(f"config-1 subset rel err {err:.3e}", flush=True)
+    assert err <= TOL_F32
+
+
+def test_rejects_bad_shapes(gpu):
+    dev = torch.device("cuda:0")
+    q = torch.zeros(4 * 3 * 64, device=dev)
+    o = torch.zeros(4 * 64, device=dev)
+    lv = torch.ones(4, dtype=torch.int32, device=dev)
+    with pytest.raises(JitcastArgumentError, match="head width"):
+        chronos2.time_attention(q, o, lv, 1, 4, 1, 12, 64)
+    with pytest.raises(JitcastArgumentError, match="inner"):
+        chronos2.time_attention(q, o, lv, 1, 4, 2, 64, 64)
