@@ -72,6 +72,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=256)
+    ap.add_argument("--copy-bytes", type=int, default=0,
+                    help="only run 5 plain device copies of this many bytes (calibrates rocprof byte counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (each series and each "
@@ -85,6 +87,15 @@ def main() -> int:
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.copy_bytes:
+        a = torch.empty(args.copy_bytes // 4, dtype=torch.float32, device=dev).fill_(1.0)
+        b = torch.empty_like(a)
+        torch.cuda.synchronize()
+        for _ in range(5):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        log(f"copied {args.copy_bytes} bytes 5 times")
+        return 0
     log("generating config 1 inputs in HBM")
     case = synthetic.c2_time_config1(device="cuda")
     out = torch.empty(case.rows * case.n, case.inner, dtype=torch.float32, device=dev)

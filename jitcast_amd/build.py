@@ -28,6 +28,9 @@ COMMON = [
     "-fPIC",
     f"--offload-arch={ARCH}",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in VGPRs: the softmax and rescale read them with VALU ops, which cannot
+    # address AGPRs (the AGPR form costs a v_accvgpr copy per element per block)
+    "-mllvm", "--amdgpu-mfma-vgpr-form",
     "-Wall",
     "-Wno-unused-function",
     "-Wno-unused-command-line-argument",

@@ -222,6 +222,8 @@ int jc_c2_time_attention(jc_ctx* ctx, const void* qkv, void* out, const int32_t*
     if (!aligned16(qkv) || !aligned16(out) || (table && !aligned16(table)))
         return fail(JC_EINVAL, "%s: qkv, out and rope_table must be 16-byte aligned", W);
     if ((uint64_t)rows * heads * ((n + 127) / 128) > 0x7fffffffull) return fail(JC_EINVAL, "%s: grid too large", W);
+    if ((uint64_t)n * 3 * inner * dtype_size(dtype) >= 0x80000000ull)
+        return fail(JC_EINVAL, "%s: one row of qkv (n*3*inner) must stay under 2 GiB", W);
     hipError_t e;
     if (dtype == JC_F32) {
         e = jc::c2_time_attention_f32_launch((const float*)qkv, (float*)out, live, table, rows, n, heads, dh, inner,
