@@ -65,6 +65,56 @@ def cpu_baseline(case, sample_rows: int, threads: int):
     }
 
 
+def time_launches(fn, steps: int, warmup: int):
+    """Average launch time (ms) over `steps` launches, HIP events on the launch stream."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for a, b in ev:
+        a.record(stream)
+        fn()
+        b.record(stream)
+    torch.cuda.synchronize()
+    return sum(a.elapsed_time(b) for a, b in ev) / len(ev)
+
+
+def group_attention_line(steps: int, warmup: int) -> dict:
+    """Config 2: fp32 group attention, 4096 rows x 129 slots, groups U{1..64}; HBM-bound."""
+    import torch
+
+    from jitcast_amd import chronos2, synthetic
+
+    case = synthetic.c2_group_config2(device="cuda")
+    out = torch.empty(case.rows * case.n, case.inner, dtype=torch.float32, device="cuda")
+
+    def fn():
+        chronos2.group_attention(case.qkv, out, case.live, case.group_start, case.group_end, case.rows, case.n,
+                                 case.heads, case.dh, case.inner)
+
+    ms = time_launches(fn, steps, warmup)
+    nbytes = case.algorithmic_bytes()
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    log(f"group attention: {ms:.4f} ms, {gbs:.0f} GB/s algorithmic ({100 * gbs / PEAK_HBM_GBS:.1f}% of HBM)")
+    res = {
+        "workload": "config 2: fp32 Chronos-2 group attention, 4096 rows x 129 slots, 12x64, groups U{1..64}",
+        "kernel": "c2_group_attention_f32<64>",
+        "launch_ms": round(ms, 5),
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": traffic_from_profile("c2_group_attention_f32_config2")},
+        "bytes_per_launch": nbytes,
+        "tflops": round(case.flops() / (ms * 1e-3) / 1e12, 2),
+    }
+    del case, out
+    torch.cuda.empty_cache()
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -72,6 +122,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=256)
+    ap.add_argument("--only", choices=["all", "time", "group"], default="all",
+                    help="which workloads to run (profiling runs select one kernel)")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="only run 5 plain device copies of this many bytes (calibrates rocprof byte counters)")
     args = ap.parse_args()
@@ -96,6 +148,12 @@ def main() -> int:
         torch.cuda.synchronize()
         log(f"copied {args.copy_bytes} bytes 5 times")
         return 0
+    also = {}
+    if args.only in ("all", "group"):
+        also["c2_group_attention_f32"] = group_attention_line(max(5, args.steps // 2), 2)
+        if args.only == "group":
+            print(json.dumps({"also": also}), flush=True)
+            return 0
     log("generating config 1 inputs in HBM")
     case = synthetic.c2_time_config1(device="cuda")
     out = torch.empty(case.rows * case.n, case.inner, dtype=torch.float32, device=dev)
@@ -169,6 +227,7 @@ def main() -> int:
             "launch_ms": round(launch_ms, 5),
         },
         "cpu_baseline": cpu,
+        "also": also,
     }
     print(json.dumps(line), flush=True)
     return 0

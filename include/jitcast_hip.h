@@ -111,6 +111,42 @@ int jc_c2_rope_table(int n, int dh, float theta, float *table_host);
 int jc_c2_time_attention(jc_ctx *ctx, const void *qkv, void *out, const int32_t *live, const float *rope_table,
                          int rows, int n, int heads, int dh, int inner, int dtype);
 
+/* ---- Chronos-2 group attention ---------------------------------------------------------------- */
+
+/*
+ * Attention across the rows of each group at every token slot, per head: row i reads the rows j
+ * in [group_start[i], group_end[i]) whose token at the slot is live; unscaled scores, no RoPE;
+ * zeros when none is. Groups must be contiguous runs of rows (jc_c2_group_order makes them so).
+ * Replaces Chronos2Kernels.groupAttention(qkv, out, live, groupStart, groupEnd, rows, n, heads,
+ * dh, inner) (J/chronos2/tornado/Chronos2Kernels.java:473-474), oracle CpuChronos2.java:230-282.
+ *   qkv, out     device, as jc_c2_time_attention (the group sublayer's own projection)
+ *   group_start  device int32 [rows]; group_end device int32 [rows] (jc_c2_group_bounds)
+ *   dh           a multiple of 16, at most 64
+ */
+int jc_c2_group_attention(jc_ctx *ctx, const void *qkv, void *out, const int32_t *live, const int32_t *group_start,
+                          const int32_t *group_end, int rows, int n, int heads, int dh, int inner, int dtype);
+
+/* ---- host-side layout (the per-call work the reference does in Java before each upload) ------- */
+
+/*
+ * live[i*n + p] for n = nc + reg + h tokens: a context patch is live when any of its `patch`
+ * steps of window[i*nc*patch ..] is not NaN; [REG] and future tokens are always live.
+ * Replaces ModelLayout.of's mask (J/chronos2/ModelLayout.java:104-114). Host memory.
+ */
+int jc_c2_live(const float *window, int rows, int nc, int patch, int reg, int h, int32_t *live);
+/*
+ * The row order that makes groups contiguous: groups in order of first appearance, rows in order
+ * within a group; *identity = 1 when the rows already are. Replaces Chronos2Forward.groupOrder
+ * (J/chronos2/tornado/Chronos2Forward.java:178-194). Host memory.
+ */
+int jc_c2_group_order(const int32_t *group, int rows, int32_t *order, int *identity);
+/*
+ * Per-row [start, end) of each row's group; JC_EINVAL if a group's rows are not contiguous.
+ * Replaces the bounds fill of Chronos2Forward.Plan.run (J/chronos2/tornado/Chronos2Forward.java:475-489)
+ * and TimestralForward.Plan.run's contiguity check (J/timestral/tornado/TimestralForward.java:614-629).
+ */
+int jc_c2_group_bounds(const int32_t *group, int rows, int32_t *start, int32_t *end);
+
 #ifdef __cplusplus
 }
 #endif

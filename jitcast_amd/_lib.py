@@ -57,6 +57,10 @@ SIGNATURES = {
     "jc_fill_uniform": (_i, [_vp, _vp, _c.c_uint64, _c.c_uint64, _f, _f]),
     "jc_c2_rope_table": (_i, [_i, _i, _f, _vp]),
     "jc_c2_time_attention": (_i, [_vp, _vp, _vp, _i32p, _vp, _i, _i, _i, _i, _i, _i]),
+    "jc_c2_group_attention": (_i, [_vp, _vp, _vp, _i32p, _i32p, _i32p, _i, _i, _i, _i, _i, _i]),
+    "jc_c2_live": (_i, [_vp, _i, _i, _i, _i, _i, _vp]),
+    "jc_c2_group_order": (_i, [_vp, _i, _vp, _c.POINTER(_i)]),
+    "jc_c2_group_bounds": (_i, [_vp, _i, _vp, _vp]),
 }
 
 _lib = None

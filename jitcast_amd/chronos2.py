@@ -5,7 +5,9 @@ on the GPU, and launches on torch's current stream:
 
   time_attention   Chronos2Kernels.rope + Chronos2Kernels.timeAttention
                    (J/chronos2/tornado/Chronos2Kernels.java:93-94, 130-131), fused
+  group_attention  Chronos2Kernels.groupAttention (Chronos2Kernels.java:473-474)
   rope_table       the host-built table of Chronos2Forward.Plan.run (Chronos2Forward.java:465-474)
+  live_mask, group_order, group_bounds   ModelLayout.java:104-114, Chronos2Forward.java:178-194, 475-489
 """
 from __future__ import annotations
 
@@ -49,3 +51,47 @@ def time_attention(qkv, out, live, rows: int, n: int, heads: int, dh: int, inner
     ctx = context(qkv.device.index or 0)
     _lib.call("jc_c2_time_attention", ctx.handle, _ptr(qkv), _ptr(out), _ptr(live), _ptr(table),
               rows, n, heads, dh, inner, dt)
+
+
+def group_attention(qkv, out, live, group_start, group_end, rows: int, n: int, heads: int, dh: int,
+                    inner: int) -> None:
+    """Attention across the rows of each group at every slot (Chronos2Kernels.groupAttention).
+
+    group_start/group_end: int32 [rows] device tensors (see group_bounds); groups contiguous.
+    """
+    dt = _dtype_code(qkv)
+    if _dtype_code(out) != dt:
+        raise _lib.JitcastArgumentError(_lib.JC_EINVAL, "qkv and out must have the same dtype")
+    ctx = context(qkv.device.index or 0)
+    _lib.call("jc_c2_group_attention", ctx.handle, _ptr(qkv), _ptr(out), _ptr(live), _ptr(group_start),
+              _ptr(group_end), rows, n, heads, dh, inner, dt)
+
+
+def live_mask(window: np.ndarray, nc: int, patch: int, reg: int, h: int) -> np.ndarray:
+    """ModelLayout's live mask [rows, nc+reg+h] int32 from the NaN-padded window [rows, nc*patch]."""
+    w = np.ascontiguousarray(window, dtype=np.float32)
+    rows = w.shape[0]
+    out = np.empty((rows, nc + reg + h), np.int32)
+    _lib.call("jc_c2_live", w.ctypes.data_as(ctypes.c_void_p), rows, nc, patch, reg, h,
+              out.ctypes.data_as(ctypes.c_void_p))
+    return out
+
+
+def group_order(group) -> np.ndarray | None:
+    """Row order making groups contiguous (Chronos2Forward.groupOrder); None if already contiguous."""
+    g = np.ascontiguousarray(group, dtype=np.int32)
+    order = np.empty(len(g), np.int32)
+    ident = ctypes.c_int()
+    _lib.call("jc_c2_group_order", g.ctypes.data_as(ctypes.c_void_p), len(g), order.ctypes.data_as(ctypes.c_void_p),
+              ctypes.byref(ident))
+    return None if ident.value else order
+
+
+def group_bounds(group) -> tuple[np.ndarray, np.ndarray]:
+    """Per-row [start, end) of each row's (contiguous) group; raises if a group is split."""
+    g = np.ascontiguousarray(group, dtype=np.int32)
+    start = np.empty(len(g), np.int32)
+    end = np.empty(len(g), np.int32)
+    _lib.call("jc_c2_group_bounds", g.ctypes.data_as(ctypes.c_void_p), len(g), start.ctypes.data_as(ctypes.c_void_p),
+              end.ctypes.data_as(ctypes.c_void_p))
+    return start, end

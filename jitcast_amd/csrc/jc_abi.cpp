@@ -52,6 +52,16 @@ size_t dtype_size(int dtype) { return dtype == JC_F32 ? 4 : 2; }
 
 }  // namespace
 
+namespace jc {
+int host_fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return code;
+}
+}  // namespace jc
+
 extern "C" {
 
 const char* jc_last_error(void) { return g_err; }
@@ -228,6 +238,31 @@ int jc_c2_time_attention(jc_ctx* ctx, const void* qkv, void* out, const int32_t*
     if (dtype == JC_F32) {
         e = jc::c2_time_attention_f32_launch((const float*)qkv, (float*)out, live, table, rows, n, heads, dh, inner,
                                              ctx->stream);
+    } else {
+        return fail(JC_EUNSUPPORTED, "%s: dtype %d is not built yet", W, dtype);
+    }
+    return e == hipSuccess ? JC_OK : hip_fail(W, e);
+}
+
+int jc_c2_group_attention(jc_ctx* ctx, const void* qkv, void* out, const int32_t* live, const int32_t* group_start,
+                          const int32_t* group_end, int rows, int n, int heads, int dh, int inner, int dtype) {
+    const char* W = "jc_c2_group_attention";
+    int rc = use(ctx, W);
+    if (rc) return rc;
+    if (rows < 0 || n < 0 || heads < 1) return fail(JC_EINVAL, "%s: bad shape rows=%d n=%d heads=%d", W, rows, n, heads);
+    if (dh < 16 || dh > 64 || dh % 16)
+        return fail(JC_EINVAL, "%s: head width %d (need a multiple of 16, <= 64)", W, dh);
+    if (inner < heads * dh || inner % 4)
+        return fail(JC_EINVAL, "%s: inner %d (need >= heads*dh = %d and a multiple of 4)", W, inner, heads * dh);
+    if (dtype != JC_F32 && dtype != JC_BF16 && dtype != JC_F16) return fail(JC_EINVAL, "%s: dtype %d", W, dtype);
+    if ((size_t)rows * n == 0) return JC_OK;
+    if (!qkv || !out || !live || !group_start || !group_end) return fail(JC_EINVAL, "%s: null device pointer", W);
+    if (!aligned16(qkv) || !aligned16(out)) return fail(JC_EINVAL, "%s: qkv and out must be 16-byte aligned", W);
+    if ((uint64_t)((rows + 15) / 16) * n > 0x7fffffffull) return fail(JC_EINVAL, "%s: grid too large", W);
+    hipError_t e;
+    if (dtype == JC_F32) {
+        e = jc::c2_group_attention_f32_launch((const float*)qkv, (float*)out, live, group_start, group_end, rows, n,
+                                              heads, dh, inner, ctx->stream);
     } else {
         return fail(JC_EUNSUPPORTED, "%s: dtype %d is not built yet", W, dtype);
     }

@@ -10,6 +10,9 @@ namespace jc {
 hipError_t c2_time_attention_f32_launch(const float* qkv, float* out, const int32_t* live, const float* table,
                                         int rows, int n, int heads, int dh, int inner, hipStream_t stream);
 int c2_time_attention_max_tokens();
+hipError_t c2_group_attention_f32_launch(const float* qkv, float* out, const int32_t* live, const int32_t* gs,
+                                         const int32_t* ge, int rows, int n, int heads, int dh, int inner,
+                                         hipStream_t stream);
 
 hipError_t fill_normal_launch(float* out, uint64_t count, uint64_t stream_seed, double mean, double stdv,
                               hipStream_t stream);

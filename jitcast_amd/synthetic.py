@@ -55,3 +55,46 @@ def c2_time_config1(rows: int = 256, n: int = 513, heads: int = 12, dh: int = 64
     live_t = torch.from_numpy(live.reshape(-1)).to(device)
     table = torch.from_numpy(rope_table(n, dh)).to(device)
     return TimeCase(rows, n, heads, dh, inner, qkv.contiguous(), live_t, table, pads)
+
+
+@dataclass
+class GroupCase:
+    rows: int
+    n: int
+    heads: int
+    dh: int
+    inner: int
+    qkv: object  # torch [rows*n, 3*inner]
+    live: object  # torch int32 [rows*n]
+    group_start: object  # torch int32 [rows]
+    group_end: object
+    group: np.ndarray
+
+    def algorithmic_bytes(self) -> float:
+        """Read q, k, v once and write out once, fp32: rows*n*(3*inner + inner)*4."""
+        return float(self.rows) * self.n * 4 * self.inner * 4
+
+    def flops(self) -> float:
+        """QK^T and PV over the (live) same-group pairs of every slot: 4*dh per pair per head."""
+        sizes = np.bincount(self.group)
+        live_slots = self.live.view(self.rows, self.n).sum().item() / self.rows  # all live in config 2
+        return 4.0 * self.dh * self.heads * float((sizes.astype(np.float64) ** 2).sum()) * live_slots
+
+
+def c2_group_config2(rows: int = 4096, n: int = 129, heads: int = 12, dh: int = 64, lo: int = 1, hi: int = 64,
+                     seed: int = 0, device: str = "cuda") -> GroupCase:
+    """Config 2: qkv ~ N(0,1) [rows*n, 3*inner]; contiguous groups with sizes U{lo..hi} (the last
+    truncated); every slot live."""
+    import torch
+
+    from .chronos2 import group_bounds
+
+    inner = heads * dh
+    qkv = torch.empty(rows * n, 3 * inner, dtype=torch.float32, device=device)
+    fill_normal(qkv, rng.stream_seed(seed, 0), 0.0, 1.0)
+    sizes = rng.randint(rng.stream_seed(seed, 3), rows, lo, hi)
+    group = np.repeat(np.arange(rows, dtype=np.int32), sizes)[:rows]
+    s, e = group_bounds(group)
+    live = torch.ones(rows * n, dtype=torch.int32, device=device)
+    return GroupCase(rows, n, heads, dh, inner, qkv, live, torch.from_numpy(s).to(device),
+                     torch.from_numpy(e).to(device), group)

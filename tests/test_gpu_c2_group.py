@@ -1,0 +1,71 @@
+"""GPU parity of Chronos-2 group attention against the C oracle (through the C ABI). Bar: max
+relative error <= 1e-4 (fp32)."""
+import numpy as np
+import pytest
+import torch
+
+from jitcast_amd import chronos2
+from tests import cases
+
+pytestmark = pytest.mark.gpu
+TOL_F32 = 1e-4
+
+
+def _run(qkv, live, group, rows, n, heads, dh, inner):
+    dev = torch.device("cuda:0")
+    s, e = chronos2.group_bounds(group)
+    out = torch.full((rows * n, inner), float("nan"), device=dev)
+    chronos2.group_attention(torch.from_numpy(qkv).to(dev), out,
+                             torch.from_numpy(np.ascontiguousarray(live.reshape(-1), np.int32)).to(dev),
+                             torch.from_numpy(s).to(dev), torch.from_numpy(e).to(dev), rows, n, heads, dh, inner)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+CASES = [
+    # rows, n, heads, dh, inner, group sizes lo..hi, live probability
+    (37, 5, 2, 64, 128, 1, 8, 1.0),
+    (64, 3, 3, 64, 192, 1, 64, 0.8),
+    (100, 2, 2, 64, 128, 100, 100, 0.9),  # one group larger than 64 rows
+    (45, 4, 2, 32, 72, 1, 1, 0.5),  # every row its own group
+    (50, 3, 4, 16, 64, 5, 5, 0.7),
+    (33, 2, 2, 48, 100, 3, 20, 0.6),
+    (17, 1, 1, 64, 64, 17, 17, 1.0),
+]
+
+
+@pytest.mark.parametrize("rows,n,heads,dh,inner,lo,hi,p", CASES)
+def test_fp32_matches_oracle(gpu, oracle, rows, n, heads, dh, inner, lo, hi, p):
+    print(f"case rows={rows} n={n} heads={heads} dh={dh} groups {lo}..{hi} live {p}", flush=True)
+    qkv = cases.qkv(41, rows * n, inner)
+    live = cases.random_live(41, rows, n, p)
+    group = cases.group_sizes(41, rows, lo, hi)
+    got = _run(qkv, live, group, rows, n, heads, dh, inner)[:, : heads * dh]
+    exp = oracle.c2_group_attention(qkv, live, group, rows, n, heads, dh, inner)[:, : heads * dh]
+    assert np.isfinite(got).all()
+    assert oracle.rel_max_error(got, exp) <= TOL_F32
+
+
+def test_fp32_unobserved_slot_gives_zeros(gpu, oracle):
+    rows, n, heads, dh, inner = 20, 4, 2, 64, 128
+    qkv = cases.qkv(43, rows * n, inner)
+    group = np.repeat(np.arange(4, dtype=np.int32), 5)
+    live = np.ones((rows, n), np.int32)
+    live[5:10, 2] = 0  # group 1 sees nothing at slot 2
+    got = _run(qkv, live, group, rows, n, heads, dh, inner).reshape(rows, n, inner)
+    assert not np.any(got[5:10, 2])
+    exp = oracle.c2_group_attention(qkv, live, group, rows, n, heads, dh, inner)
+    assert oracle.rel_max_error(got.reshape(rows * n, inner), exp) <= TOL_F32
+
+
+def test_fp32_config2_shape_subset(gpu, oracle):
+    """Config 2's shape (129 slots, 12x64, groups U{1..64}) on 256 rows with all slots live."""
+    rows, n, heads, dh, inner = 256, 129, 12, 64, 768
+    qkv = cases.qkv(47, rows * n, inner)
+    live = np.ones((rows, n), np.int32)
+    group = cases.group_sizes(47, rows, 1, 64)
+    got = _run(qkv, live, group, rows, n, heads, dh, inner)
+    exp = oracle.c2_group_attention(qkv, live, group, rows, n, heads, dh, inner)
+    err = oracle.rel_max_error(got, exp)
+    print(f"config-2 subset rel err {err:.3e}", flush=True)
+    assert err <= TOL_F32
