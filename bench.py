@@ -149,7 +149,7 @@ def main() -> int:
         log(f"copied {args.copy_bytes} bytes 5 times")
         return 0
     also = {}
-    if args.only in ("all", "group"):
+    if args.only in ("all", "group") and args.only != "time":
         also["c2_group_attention_f32"] = group_attention_line(max(5, args.steps // 2), 2)
         if args.only == "group":
             print(json.dumps({"also": also}), flush=True)

@@ -7,10 +7,14 @@
 // key is live.
 //
 // The stage reads q|k|v once and writes out once, about 10 flop per byte: it is HBM-bound, so the
-// kernel is built around the memory stream. One wave per (16-row tile, slot) loops over the heads
-// with everything in registers (no LDS, no barriers): per head it loads the tile's queries and the
-// keys/values of the union of the tile's groups straight into MFMA operand layout, and runs
-// v_mfma_f32_16x16x4_f32 tiles with an online softmax over 16-key tiles, so any group size works.
+// kernel is built around the memory stream. One wave per (16-row tile, slot) owns the groups that
+// START in its tile (found by a ballot on groupStart[i] == i), so each row's q, k and v are fetched
+// from HBM once; everything lives in registers (no LDS, no barriers). The wave's work is a flat
+// stream of jobs (group, chunk of up to 4 query tiles, head, 16-key tile): the chunk's queries and
+// output accumulators stay in registers while the group's key tiles stream past, each K/V tile used
+// by every query tile right after it lands, and the next job's K/V loads are issued before this
+// job's MFMAs (register double-buffering). The online softmax across key tiles makes any group size
+// work; a group past 64 rows re-streams its keys once per further 64-row chunk.
 //
 // Operand layouts (16x16x4 f32: A lane i+16kk = A[i][kk], B lane j+16kk = B[kk][j],
 // D lane j+16g reg r = D[4g+r][j]):
@@ -24,7 +28,7 @@
 namespace jc {
 namespace {
 
-constexpr int kRT = 16;  // rows (queries) per tile
+constexpr int kRT = 16;  // rows per tile (queries and keys)
 
 // max / sum over the four lanes j, j+16, j+32, j+48 (v_permlane16_swap then v_permlane32_swap)
 __device__ __forceinline__ float quad_max(float v) {
@@ -38,6 +42,16 @@ __device__ __forceinline__ float quad_sum(float v) {
     v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
     return pair_sum(v);
 }
+
+// A position in the wave's job stream: group [gs, ge), query chunk qc (up to kQT tiles of 16
+// rows), head h, key tile kt.
+struct Job {
+    int gs, ge, qc, h, kt;
+    uint32_t rest;  // starts of the tile's remaining groups (bit b = row r0 + b)
+    bool valid;
+};
+
+constexpr int kQT = 4;  // query tiles held in registers at once (64 rows)
 
 template <int DH>
 __global__ __launch_bounds__(kWave) void c2_group_attention_f32(const float* __restrict__ qkv, float* __restrict__ out,
@@ -57,90 +71,139 @@ __global__ __launch_bounds__(kWave) void c2_group_attention_f32(const float* __r
     const size_t stride = 3 * (size_t)inner;  // floats per token of qkv
     const size_t tok_n = (size_t)n;
 
-    // this lane's query row and its group; the key range is the union of the tile's groups
-    const bool qvalid = j < nr;
-    const int qrow = r0 + (qvalid ? j : nr - 1);
-    const int gs_q = gstart[qrow], ge_q = gend[qrow];
-    // clamped into [0, rows]: group bounds only ever select rows that exist
-    const int ks = min(max(gstart[r0], 0), rows);
-    const int ke = min(max(gend[r0 + nr - 1], ks), rows);
+    // the groups starting in this tile
+    const uint32_t starts = (uint32_t)__ballot(lane < nr && gstart[r0 + lane] == r0 + lane) & 0xffffu;
+    if (starts == 0) return;
 
-    for (int h = 0; h < heads; h++) {
-        // Q tile: lane (j, g) holds q[r0+j][16m + 4g + u], scaled by log2(e)
-        float qreg[4 * kM];
-        {
-            const float* qp = qkv + ((size_t)qrow * tok_n + t) * stride + h * DH + 4 * g;
+    auto first_of = [&](uint32_t rest) {
+        Job jb;
+        jb.valid = rest != 0;
+        int b = jb.valid ? __builtin_ctz(rest) : 0;
+        jb.gs = r0 + b;
+        // clamped into [gs+1, rows]: a group always holds its first row and only rows that exist
+        jb.ge = jb.valid ? min(max(gend[jb.gs], jb.gs + 1), rows) : jb.gs + 1;
+        jb.qc = 0;
+        jb.h = 0;
+        jb.kt = 0;
+        jb.rest = jb.valid ? rest & (rest - 1) : 0;
+        return jb;
+    };
+    // key tiles innermost, so a K/V tile is used by every resident query tile right after it lands
+    auto advance = [&](Job jb) {
+        const int tiles = (jb.ge - jb.gs + kRT - 1) / kRT;
+        if (++jb.kt < tiles) return jb;
+        jb.kt = 0;
+        if (++jb.h < heads) return jb;
+        jb.h = 0;
+        if (++jb.qc * kQT < tiles) return jb;
+        return first_of(jb.rest);
+    };
+    // K (A operand) and V^T (A operand of PV) of a job's key tile; rows past the group are clamped
+    // (finite, masked). live bit of key 16kt + j in lanes j < 16.
+    struct Kv {
+        floatx4 k[kM];
+        float v[kM][4];
+        int live;
+    };
+    auto load_kv = [&](const Job& jb, Kv& d) {
+        const int kbase = jb.gs + kRT * jb.kt;
+        const int krow = min(kbase + j, jb.ge - 1);
+        const float* kp = qkv + ((size_t)krow * tok_n + t) * stride + inner + jb.h * DH + 4 * g;
+        d.live = (g == 0 && kbase + j < jb.ge) ? live[(size_t)krow * tok_n + t] : 0;
 #pragma unroll
-            for (int m = 0; m < kM; m++) {
-                floatx4 a = *reinterpret_cast<const floatx4*>(qp + 16 * m);
+        for (int m = 0; m < kM; m++) d.k[m] = *reinterpret_cast<const floatx4*>(kp + 16 * m);
 #pragma unroll
-                for (int u = 0; u < 4; u++) qreg[4 * m + u] = qvalid ? a[u] * kLog2e : 0.f;
+        for (int c = 0; c < 4; c++) {
+            const int vrow = min(kbase + 4 * g + c, jb.ge - 1);
+            const float* vp = qkv + ((size_t)vrow * tok_n + t) * stride + 2 * inner + jb.h * DH + j;
+#pragma unroll
+            for (int m = 0; m < kM; m++) d.v[m][c] = vp[16 * m];
+        }
+    };
+
+    Job cur = first_of(starts);
+    Kv dc, dn;
+    load_kv(cur, dc);
+
+    float qreg[kQT][4 * kM];  // resident query tiles (B operand), scaled by log2(e)
+    floatx4 o_acc[kQT][kM];
+    float m_run[kQT], l_run[kQT];
+    while (cur.valid) {
+        const int tiles = (cur.ge - cur.gs + kRT - 1) / kRT;
+        const int nq = min(kQT, tiles - kQT * cur.qc);  // query tiles in this chunk
+        if (cur.kt == 0) {
+            // a new (group, chunk, head): load its query tiles and reset the softmax state
+#pragma unroll
+            for (int qi = 0; qi < kQT; qi++) {
+                if (qi < nq) {
+                    const int qrow = min(cur.gs + kRT * (kQT * cur.qc + qi) + j, cur.ge - 1);
+                    const float* qp = qkv + ((size_t)qrow * tok_n + t) * stride + cur.h * DH + 4 * g;
+#pragma unroll
+                    for (int m = 0; m < kM; m++) {
+                        floatx4 a = *reinterpret_cast<const floatx4*>(qp + 16 * m);
+#pragma unroll
+                        for (int u = 0; u < 4; u++) qreg[qi][4 * m + u] = a[u] * kLog2e;
+                    }
+                }
+#pragma unroll
+                for (int m = 0; m < kM; m++) o_acc[qi][m] = floatx4{0.f, 0.f, 0.f, 0.f};
+                m_run[qi] = -INFINITY;
+                l_run[qi] = 0.f;
             }
         }
-        floatx4 o_acc[kM];
-#pragma unroll
-        for (int m = 0; m < kM; m++) o_acc[m] = floatx4{0.f, 0.f, 0.f, 0.f};
-        float m_run = -INFINITY, l_run = 0.f;
+        const Job nxt = advance(cur);
+        load_kv(nxt, dn);  // in flight under this job's MFMAs (an invalid job reloads in-bounds rows)
+        __builtin_amdgcn_sched_barrier(0);
 
-        for (int kt = ks; kt < ke; kt += 16) {
-            // K tile (A operand): lane (i, g) holds k[kt+i][16m + 4g + u]; rows past ke are clamped
-            // (finite, masked below)
-            const int krow = min(kt + j, ke - 1);
-            const float* kp = qkv + ((size_t)krow * tok_n + t) * stride + inner + h * DH + 4 * g;
-            floatx4 kreg[kM];
+        const uint32_t lbits = (uint32_t)__ballot(dc.live != 0) & 0xffffu;  // bit b: key gs + 16kt + b
 #pragma unroll
-            for (int m = 0; m < kM; m++) kreg[m] = *reinterpret_cast<const floatx4*>(kp + 16 * m);
-            // V^T (A operand of PV): lane (i, g) holds v[key 4g + c][16m + i] for step c, dim tile m
-            float vreg[kM][4];
+        for (int qi = 0; qi < kQT; qi++) {
+            if (qi < nq) {
+                floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int c = 0; c < 4; c++) {
-                const int vrow = min(kt + 4 * g + c, ke - 1);
-                const float* vp = qkv + ((size_t)vrow * tok_n + t) * stride + 2 * inner + h * DH + j;
+                for (int m = 0; m < kM; m++)
 #pragma unroll
-                for (int m = 0; m < kM; m++) vreg[m][c] = vp[16 * m];
-            }
-            // live keys of the tile: bit b = key kt + b
-            const int lk = kt + j;
-            const uint32_t lbits =
-                (uint32_t)__ballot(g == 0 && lk < ke && live[(size_t)lk * tok_n + t] != 0) & 0xffffu;
-
-            floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f};
+                    for (int u = 0; u < 4; u++)
+                        s = __builtin_amdgcn_mfma_f32_16x16x4f32(dc.k[m][u], qreg[qi][4 * m + u], s, 0, 0, 0);
+                // reg r of lane (j, g) is key 16kt + 4g + r of the group (every row of the job is in it)
 #pragma unroll
-            for (int m = 0; m < kM; m++)
+                for (int r = 0; r < 4; r++) s[r] = ((lbits >> (4 * g + r)) & 1u) ? s[r] : -INFINITY;
+                const float mx = quad_max(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])));
+                const float m_new = fmaxf(m_run[qi], mx);
+                const float m_use = m_new == -INFINITY ? 0.f : m_new;
+                const float alpha = fast_exp2(m_run[qi] - m_use);
+                m_run[qi] = m_new;
 #pragma unroll
-                for (int u = 0; u < 4; u++) s = __builtin_amdgcn_mfma_f32_16x16x4f32(kreg[m][u], qreg[4 * m + u], s, 0, 0, 0);
-
-            // reg r of lane (j, g) is key kt + 4g + r for query r0 + j
+                for (int r = 0; r < 4; r++) s[r] = fast_exp2(s[r] - m_use);
+                l_run[qi] = l_run[qi] * alpha + (s[0] + s[1]) + (s[2] + s[3]);
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int key = kt + 4 * g + r;
-                const bool ok = qvalid && ((lbits >> (4 * g + r)) & 1u) && key >= gs_q && key < ge_q;
-                s[r] = ok ? s[r] : -INFINITY;
-            }
-            float mx = quad_max(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])));
-            const float m_new = fmaxf(m_run, mx);
-            const float m_use = m_new == -INFINITY ? 0.f : m_new;
-            const float alpha = fast_exp2(m_run - m_use);
-            m_run = m_new;
+                for (int m = 0; m < kM; m++) {
+                    o_acc[qi][m] *= alpha;
 #pragma unroll
-            for (int r = 0; r < 4; r++) s[r] = fast_exp2(s[r] - m_use);
-            l_run = l_run * alpha + (s[0] + s[1]) + (s[2] + s[3]);
-#pragma unroll
-            for (int m = 0; m < kM; m++) {
-                o_acc[m] *= alpha;
-#pragma unroll
-                for (int c = 0; c < 4; c++) o_acc[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(vreg[m][c], s[c], o_acc[m], 0, 0, 0);
+                    for (int c = 0; c < 4; c++)
+                        o_acc[qi][m] = __builtin_amdgcn_mfma_f32_16x16x4f32(dc.v[m][c], s[c], o_acc[qi][m], 0, 0, 0);
+                }
             }
         }
 
-        const float l = quad_sum(l_run);
-        if (qvalid) {
-            const float inv = l > 0.f ? 1.f / l : 0.f;
-            float* op = out + ((size_t)(r0 + j) * tok_n + t) * inner + h * DH + 4 * g;
-            // O^T reg r of lane (j, g) in dim tile m is dim 16m + 4g + r of query r0 + j
+        if (cur.kt == tiles - 1) {
 #pragma unroll
-            for (int m = 0; m < kM; m++) *reinterpret_cast<floatx4*>(op + 16 * m) = o_acc[m] * inv;
+            for (int qi = 0; qi < kQT; qi++) {
+                if (qi < nq) {
+                    const float l = quad_sum(l_run[qi]);
+                    const int qrow = cur.gs + kRT * (kQT * cur.qc + qi) + j;
+                    if (qrow < cur.ge) {
+                        const float inv = l > 0.f ? 1.f / l : 0.f;
+                        float* op = out + ((size_t)qrow * tok_n + t) * inner + cur.h * DH + 4 * g;
+                        // O^T reg r of lane (j, g) in dim tile m is dim 16m + 4g + r of the query
+#pragma unroll
+                        for (int m = 0; m < kM; m++) *reinterpret_cast<floatx4*>(op + 16 * m) = o_acc[qi][m] * inv;
+                    }
+                }
+            }
         }
+        cur = nxt;
+        dc = dn;
     }
 }
 
