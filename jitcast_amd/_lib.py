@@ -79,7 +79,7 @@ def lib() -> ctypes.CDLL:
         path = Path(os.environ.get("JITCAST_HIP_LIB", LIB_PATH))
         if not path.exists():
             raise LibraryMissing(
-                f"{path} is not built; run `python -m jitcast_amd.build` (or __graft_entry__.build())")
+                f"{path} is not built; run `python jitcast_amd/build.py` (or __graft_entry__.build())")
         # One HIP runtime per process: torch ships libamdhip64.so with SONAME libamdhip64.so.7. Loading
         # torch first lets the dynamic loader resolve this library's libamdhip64.so.7 to that same
         # copy, so device pointers and streams are shared. Without torch, /opt/rocm's runtime loads.

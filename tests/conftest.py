@@ -44,7 +44,10 @@ def gpu():
 @pytest.fixture(scope="session", autouse=True)
 def _built_library():
     """CPU tests load libjitcast_hip (symbols, host helpers); build it once if this tree has none."""
-    from jitcast_amd import build as b
+    import importlib.util
 
+    spec = importlib.util.spec_from_file_location("jitcast_amd_build", ROOT / "jitcast_amd" / "build.py")
+    b = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(b)
     if not b.LIB.exists():
         b.build(verbose=False)
