@@ -20,6 +20,7 @@ from pathlib import Path
 
 ROOT = Path(__file__).resolve().parent
 PEAK_FP32_TFLOPS = 157.3
+PEAK_BF16_TFLOPS = 2516.6
 PEAK_HBM_GBS = 8000.0
 METRIC = "fused attention TFLOP/s (% MFMA peak) at L=513, 12x64 heads; forecast series/sec"
 
@@ -115,6 +116,41 @@ def group_attention_line(steps: int, warmup: int) -> dict:
     return res
 
 
+def time_attention_lowp_line(case, steps: int, warmup: int, dtype_name: str) -> dict:
+    """Config 1-bf16 (or fp16): the config-1 inputs with qkv rounded to the storage type (what a
+    projection epilogue writing bf16 hands over); fp32 accumulation and softmax."""
+    import torch
+
+    from jitcast_amd import chronos2
+
+    dt = {"bf16": torch.bfloat16, "fp16": torch.float16}[dtype_name]
+    q16 = case.qkv.to(dt)
+    out = torch.empty(case.rows * case.n, case.inner, dtype=dt, device=q16.device)
+
+    def fn():
+        chronos2.time_attention(q16, out, case.live, case.rows, case.n, case.heads, case.dh, case.inner, case.table)
+
+    ms = time_launches(fn, steps, warmup)
+    flops = case.mask_aware_flops()
+    tf = flops / (ms * 1e-3) / 1e12
+    log(f"time attention {dtype_name}: {ms:.4f} ms, {tf:.1f} TFLOP/s mask-aware "
+        f"({100 * tf / PEAK_BF16_TFLOPS:.1f}% of the {dtype_name} MFMA peak)")
+    res = {
+        "workload": f"config 1-{dtype_name}: the config-1 inputs with qkv in {dtype_name}, fp32 accumulation",
+        "kernel": f"c2_time_attention_lp<{dtype_name},64>",
+        "launch_ms": round(ms, 5),
+        "value": round(tf, 2),
+        "unit": "TFLOP/s",
+        "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tf / PEAK_BF16_TFLOPS, 4),
+                     "traffic": traffic_from_profile(f"c2_time_attention_{dtype_name}_config1")},
+        "dense_tflops": round(case.dense_flops() / (ms * 1e-3) / 1e12, 2),
+    }
+    del q16, out
+    torch.cuda.empty_cache()
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -122,7 +158,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=256)
-    ap.add_argument("--only", choices=["all", "time", "group"], default="all",
+    ap.add_argument("--only", choices=["all", "time", "group", "bf16", "fp16"], default="all",
                     help="which workloads to run (profiling runs select one kernel)")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="only run 5 plain device copies of this many bytes (calibrates rocprof byte counters)")
@@ -156,6 +192,12 @@ def main() -> int:
             return 0
     log("generating config 1 inputs in HBM")
     case = synthetic.c2_time_config1(device="cuda")
+    if args.only in ("all", "bf16", "fp16"):
+        for name in (("bf16", "fp16") if args.only == "all" else (args.only,)):
+            also[f"c2_time_attention_{name}"] = time_attention_lowp_line(case, args.steps, args.warmup, name)
+        if args.only != "all":
+            print(json.dumps({"also": also}), flush=True)
+            return 0
     out = torch.empty(case.rows * case.n, case.inner, dtype=torch.float32, device=dev)
     flops = case.mask_aware_flops()
     dense = case.dense_flops()

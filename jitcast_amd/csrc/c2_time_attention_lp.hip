@@ -1,0 +1,461 @@
+// Chronos-2 time attention, fused flash-style for gfx950: the bf16 / fp16 path (fp32 accumulation,
+// fp32 softmax).
+//
+// Same contract as the fp32 kernel (c2_time_attention.hip; reference Chronos2Kernels.rope +
+// Chronos2Kernels.timeAttention, Chronos2Kernels.java:87-116, 118-464; oracle CpuChronos2.java:
+// 175-228, 284-304): for every (row r, head h, query t), s_k = q_t . k_k over the keys k with
+// live[r*n+k] (unscaled, both directions), o_t = sum_k softmax(s)_k v_k, zeros when no key is live.
+// RoPE rotates q and k at load from the fp32 table [n, dh] (the rotation runs in fp32, then rounds
+// to the storage type). qkv and out are bf16 or fp16; scores, softmax and accumulation are fp32.
+//
+// Layout: qkv [rows*n, 3*inner], out [rows*n, inner], live [rows*n] int32. One workgroup = NW
+// waves = NW*32 consecutive queries of one (row, head); keys stream through LDS in 64-key blocks,
+// double-buffered, from the row's first live key; all-dead blocks are skipped.
+//
+// MFMA mapping (v_mfma_f32_32x32x16_{bf16,f16}: A lane i+32g holds A[i][8g..8g+7], B lane j+32g
+// holds B[8g..8g+7][j], D lane j+32g reg r = D[8(r/4)+4g+r%4][j]):
+//   S^T[key][q] = K Q^T   step s contracts dims 16s+8g..+7: A = K rows from LDS (one 16-byte
+//                         read), B = the wave's rotated queries, resident in registers
+//   O^T[e][q] += V^T P^T  16 keys per MFMA: B = P^T straight from S^T's accumulators (regs 8c..8c+7
+//                         of a 32-key tile are keys 16c+4g+{0..3} and 16c+8+4g+{0..3}); A = V^T
+//                         rows, stored in LDS with the keys of each 16-key group permuted
+//                         (16c+8a+4g+u -> 16c+8g+4a+u) so the same 8 keys are one 16-byte read.
+// Queries along lanes put one query's softmax state in lanes j and j+32: the block max is one
+// v_permlane32_swap.
+#include "jc_common.hpp"
+#include "jc_kernels.hpp"
+
+namespace jc {
+namespace {
+
+constexpr int kQ = 32;    // queries per wave
+constexpr int kKB = 64;   // keys per block
+constexpr int kMaxTokens = 4096;
+constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer, 32-bit data format (gfx9 family)
+
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 halfx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <typename T>
+struct Lp;
+template <>
+struct Lp<__bf16> {
+    typedef bf16x8 x8;
+    static __device__ __forceinline__ floatx16 mfma(x8 a, x8 b, floatx16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+    }
+};
+template <>
+struct Lp<_Float16> {
+    typedef halfx8 x8;
+    static __device__ __forceinline__ floatx16 mfma(x8 a, x8 b, floatx16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+    }
+};
+
+// 8 storage values <-> 8 floats (16 bytes <-> 2 float4); conversions round to nearest even
+template <typename T>
+__device__ __forceinline__ void widen8(u32x4 raw, floatx4& lo, floatx4& hi) {
+    typedef T t8 __attribute__((ext_vector_type(8)));
+    t8 v = __builtin_bit_cast(t8, raw);
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        lo[u] = (float)v[u];
+        hi[u] = (float)v[4 + u];
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ u32x4 narrow8(floatx4 lo, floatx4 hi) {
+    typedef T t8 __attribute__((ext_vector_type(8)));
+    t8 v;
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        v[u] = (T)lo[u];
+        v[4 + u] = (T)hi[u];
+    }
+    return __builtin_bit_cast(u32x4, v);
+}
+
+template <typename T>
+__device__ __forceinline__ u32x2 narrow4(floatx4 x) {
+    typedef T t4 __attribute__((ext_vector_type(4)));
+    t4 v;
+#pragma unroll
+    for (int u = 0; u < 4; u++) v[u] = (T)x[u];
+    return __builtin_bit_cast(u32x2, v);
+}
+
+template <int DH>
+struct LpLds {
+    static constexpr int kPitchK = DH + 8;         // elements per key row of K (16-byte aligned rows)
+    static constexpr int kTiles = (DH + 31) / 32;  // 32-dim output tiles
+    static constexpr int kPitchV = kKB + 8;        // elements per dim row of V^T
+    uint16_t k[2][kKB * kPitchK];
+    uint16_t vt[2][kTiles * 32 * kPitchV];
+    uint64_t mask[kMaxTokens / kKB];
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, (int)kRsrcWord3);
+}
+
+// Position of key `key` (a multiple of 4) of a block inside its V^T row: within each 16-key group,
+// key 16c + 8a + 4g + u sits at 16c + 8g + 4a + u.
+__device__ __forceinline__ int vt_pos(int key) { return (key & ~15) | ((key & 4) << 1) | ((key & 8) >> 1); }
+
+// One 64-key block of K (rotated, then rounded) and V for (row, head), staged through registers.
+//   K item (key, chunk c < dh/16): dims 8c..8c+7 and dh/2+8c..+7 (two 16-byte loads, the RoPE pair)
+//   V item (4 keys, 4 dims): four 8-byte loads, written transposed as four 8-byte V^T row pieces
+template <typename T, int DH, int NT, bool ROPE>
+struct LpStage {
+    static constexpr int kHalf = DH / 2;
+    static constexpr int kChunks = kHalf / 8;
+    static constexpr int kItemsK = kKB * kChunks;
+    static constexpr int kPerK = (kItemsK + NT - 1) / NT;
+    static constexpr int kItemsV = (kKB / 4) * (DH / 4);
+    static constexpr int kPerV = (kItemsV + NT - 1) / NT;
+    u32x4 k0[kPerK], k1[kPerK];
+    floatx4 c0[kPerK], c1[kPerK], s0[kPerK], s1[kPerK];
+    u32x2 v[kPerV][4];
+    uint32_t off_k[kPerK], off_t[kPerK], off_v[kPerV];
+
+    __device__ __forceinline__ void init(int tid, int inner) {
+        const uint32_t stride = 3u * inner * 2u;
+#pragma unroll
+        for (int i = 0; i < kPerK; i++) {
+            int it = tid + i * NT;
+            int key = it / kChunks, c = it % kChunks;
+            off_k[i] = key * stride + c * 16;
+            off_t[i] = (uint32_t)((key * DH + 8 * c) * 4);
+        }
+#pragma unroll
+        for (int i = 0; i < kPerV; i++) {
+            int it = tid + i * NT;
+            int kq = it / (DH / 4), e4 = it % (DH / 4);
+            off_v[i] = 4 * kq * stride + inner * 2 + e4 * 8;
+        }
+    }
+
+    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rt, int tid, int inner) {
+        const uint32_t stride = 3u * inner * 2u;
+#pragma unroll
+        for (int i = 0; i < kPerK; i++) {
+            if (kItemsK % NT != 0 && tid + i * NT >= kItemsK) break;
+            k0[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, off_k[i], 0, 0));
+            k1[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, off_k[i] + kHalf * 2, 0, 0));
+            if (ROPE) {
+                c0[i] = __builtin_amdgcn_raw_buffer_load_b128(rt, off_t[i], 0, 0);
+                c1[i] = __builtin_amdgcn_raw_buffer_load_b128(rt, off_t[i] + 16, 0, 0);
+                s0[i] = __builtin_amdgcn_raw_buffer_load_b128(rt, off_t[i] + kHalf * 4, 0, 0);
+                s1[i] = __builtin_amdgcn_raw_buffer_load_b128(rt, off_t[i] + kHalf * 4 + 16, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kPerV; i++) {
+            if (kItemsV % NT != 0 && tid + i * NT >= kItemsV) break;
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+                v[i][u] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rk, off_v[i] + u * stride, 0, 0));
+        }
+    }
+
+    __device__ __forceinline__ void store(LpLds<DH>& lds, int buf, int tid) {
+        constexpr int PK = LpLds<DH>::kPitchK, PV = LpLds<DH>::kPitchV;
+#pragma unroll
+        for (int i = 0; i < kPerK; i++) {
+            int it = tid + i * NT;
+            if (kItemsK % NT != 0 && it >= kItemsK) break;
+            int key = it / kChunks, c = it % kChunks;
+            u32x4 w0 = k0[i], w1 = k1[i];
+            if (ROPE) {
+                floatx4 a0, a1, b0, b1;
+                widen8<T>(k0[i], a0, a1);
+                widen8<T>(k1[i], b0, b1);
+                w0 = narrow8<T>(a0 * c0[i] - b0 * s0[i], a1 * c1[i] - b1 * s1[i]);
+                w1 = narrow8<T>(b0 * c0[i] + a0 * s0[i], b1 * c1[i] + a1 * s1[i]);
+            }
+            uint16_t* kr = &lds.k[buf][key * PK];
+            *reinterpret_cast<u32x4*>(kr + 8 * c) = w0;
+            *reinterpret_cast<u32x4*>(kr + kHalf + 8 * c) = w1;
+        }
+#pragma unroll
+        for (int i = 0; i < kPerV; i++) {
+            int it = tid + i * NT;
+            if (kItemsV % NT != 0 && it >= kItemsV) break;
+            int kq = it / (DH / 4), e4 = it % (DH / 4);
+            int pos = vt_pos(4 * kq);
+            // v[u] holds keys 4kq+u, dims 4e4..4e4+3 (two per dword); row e of V^T takes the four keys
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;  // v_perm: high or low halves
+                int w = e >> 1;
+                u32x2 row;
+                row[0] = __builtin_amdgcn_perm(v[i][1][w], v[i][0][w], sel);
+                row[1] = __builtin_amdgcn_perm(v[i][3][w], v[i][2][w], sel);
+                *reinterpret_cast<u32x2*>(&lds.vt[buf][(4 * e4 + e) * PV + pos]) = row;
+            }
+        }
+    }
+};
+
+template <typename T, int DH, int NW, bool ROPE>
+__global__ __launch_bounds__(NW * kWave) void c2_time_attention_lp(const T* __restrict__ qkv, T* __restrict__ out,
+                                                                    const int32_t* __restrict__ live,
+                                                                    const float* __restrict__ table, int rows, int n,
+                                                                    int heads, int inner, int qgroups) {
+    static_assert(DH % 16 == 0 && DH <= 64, "head width");
+    constexpr int NT = NW * kWave;
+    constexpr int kHalf = DH / 2;
+    constexpr int kSteps = DH / 16;  // QK^T MFMA steps (16 dims each)
+    constexpr int kTiles = LpLds<DH>::kTiles;
+    constexpr int kSub = kKB / 32;   // 32-key S^T tiles per block
+    constexpr int PK = LpLds<DH>::kPitchK, PV = LpLds<DH>::kPitchV;
+    typedef typename Lp<T>::x8 x8;
+    __shared__ LpLds<DH> lds;
+    __shared__ int first_live;
+
+    const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+    const int j = lane % 32, g = lane / 32;
+    const uint32_t total = (uint32_t)rows * heads * qgroups;
+    const uint32_t logical = xcd_remap(blockIdx.x, total);
+    const int qg = logical % qgroups;
+    const int bh = logical / qgroups;
+    const int h = bh % heads, r = bh / heads;
+    const int32_t* lrow = live + (size_t)r * n;
+
+    // padded V^T rows (DH not a multiple of 32) feed only discarded output dims; zero them once
+    if (DH % 32 != 0) {
+        for (int i = tid; i < 2 * kTiles * 32 * PV; i += NT) (&lds.vt[0][0])[i] = 0;
+    }
+    if (tid == 0) first_live = n;
+    __syncthreads();
+    for (int base = wave * kWave; base < n; base += NT) {
+        int k = base + lane;
+        uint64_t bits = __ballot(k < n && lrow[k] != 0);
+        if (bits && lane == 0) atomicMin(&first_live, base + (int)__builtin_ctzll(bits));
+    }
+    __syncthreads();
+    const int kstart = first_live;
+    const int nb = (n - kstart + kKB - 1) / kKB;
+    for (int kb = wave; kb * kKB < n - kstart; kb += NW) {
+        int k = kstart + kb * kKB + lane;
+        uint64_t bits = __ballot(k < n && lrow[k] != 0);
+        if (lane == 0) lds.mask[kb] = bits;
+    }
+
+    // Q in registers: lane (j, g) holds dims 16s+8g..+7 of query q0+j, rotated, scaled by log2(e),
+    // rounded to T (the B operand of step s)
+    const int q0 = (qg * NW + wave) * kQ;
+    const int nq = min(max(n - q0, 0), kQ);
+    x8 qreg[kSteps];
+    {
+        const int q = q0 + j;
+#pragma unroll
+        for (int s = 0; s < kSteps; s++) {
+            floatx4 lo = floatx4{0.f, 0.f, 0.f, 0.f}, hi = lo;
+            if (j < nq) {
+                const int d0 = 16 * s + 8 * g;
+                const T* qp = qkv + ((size_t)r * n + q) * 3 * inner + h * DH;
+                widen8<T>(*reinterpret_cast<const u32x4*>(qp + d0), lo, hi);
+                if (ROPE) {
+                    // the rotation partner of dims d0..d0+7 is the chunk half a head away
+                    const int e0 = d0 < kHalf ? d0 : d0 - kHalf;
+                    floatx4 plo, phi;
+                    widen8<T>(*reinterpret_cast<const u32x4*>(qp + (d0 < kHalf ? d0 + kHalf : e0)), plo, phi);
+                    const float* tp = table + (size_t)q * DH + e0;
+                    floatx4 c0 = *reinterpret_cast<const floatx4*>(tp), c1 = *reinterpret_cast<const floatx4*>(tp + 4);
+                    floatx4 s0 = *reinterpret_cast<const floatx4*>(tp + kHalf);
+                    floatx4 s1 = *reinterpret_cast<const floatx4*>(tp + kHalf + 4);
+                    if (d0 < kHalf) {
+                        lo = lo * c0 - plo * s0;
+                        hi = hi * c1 - phi * s1;
+                    } else {
+                        lo = lo * c0 + plo * s0;
+                        hi = hi * c1 + phi * s1;
+                    }
+                }
+                lo *= kLog2e;
+                hi *= kLog2e;
+            }
+            qreg[s] = __builtin_bit_cast(x8, narrow8<T>(lo, hi));
+        }
+    }
+    __syncthreads();
+
+    const size_t row0 = (size_t)r * n;
+    const uint32_t stride_b = 3u * inner * 2u;
+    auto rk_at = [&](int kb) {
+        int k = kstart + kb * kKB;
+        const T* p = qkv + (row0 + k) * 3 * inner + inner + h * DH;
+        uint32_t bytes = (uint32_t)(n - k) * stride_b - (uint32_t)(inner + h * DH) * 2u;
+        return make_rsrc(p, bytes);
+    };
+    auto rt_at = [&](int kb) {
+        int k = kstart + kb * kKB;
+        return make_rsrc(table + (size_t)k * DH, (uint32_t)((n - k) * DH * 4));
+    };
+
+    int kb = 0;
+    while (kb < nb && lds.mask[kb] == 0) kb++;
+
+    LpStage<T, DH, NT, ROPE> stage;
+    stage.init(tid, inner);
+    if (kb < nb) {
+        stage.load(rk_at(kb), ROPE ? rt_at(kb) : rk_at(kb), tid, inner);
+        stage.store(lds, 0, tid);
+    }
+    __syncthreads();
+
+    floatx16 o_acc[kTiles];
+#pragma unroll
+    for (int t = 0; t < kTiles; t++) o_acc[t] = floatx16{0};
+    float m_run = -INFINITY, l_run = 0.f;
+    int buf = 0;
+    // settle the prologue loads here, not inside every iteration
+    __builtin_amdgcn_s_waitcnt(0);
+
+    while (kb < nb) {
+        int next = kb + 1;
+        while (next < nb && lds.mask[next] == 0) next++;
+        if (next < nb) stage.load(rk_at(next), ROPE ? rt_at(next) : rk_at(next), tid, inner);
+        __builtin_amdgcn_sched_barrier(0);
+
+        if (nq > 0) {
+            floatx16 s_acc[kSub];
+#pragma unroll
+            for (int sb = 0; sb < kSub; sb++) {
+                s_acc[sb] = floatx16{0};
+                const uint16_t* kp = &lds.k[buf][(32 * sb + j) * PK + 8 * g];
+#pragma unroll
+                for (int s = 0; s < kSteps; s++) {
+                    x8 kv = __builtin_bit_cast(x8, *reinterpret_cast<const u32x4*>(kp + 16 * s));
+                    s_acc[sb] = Lp<T>::mfma(kv, qreg[s], s_acc[sb]);
+                }
+            }
+            // reg rho of tile sb in lane (j, g) holds key 32sb + 8*(rho/4) + 4g + rho%4 of the block
+            uint64_t km = lds.mask[kb];
+            if (km != ~0ull) {
+#pragma unroll
+                for (int sb = 0; sb < kSub; sb++) {
+#pragma unroll
+                    for (int rho = 0; rho < 16; rho++) {
+                        int bit = 32 * sb + 8 * (rho / 4) + 4 * g + (rho % 4);
+                        if (!((km >> bit) & 1ull)) s_acc[sb][rho] = -INFINITY;
+                    }
+                }
+            }
+            float mx = s_acc[0][0];
+#pragma unroll
+            for (int sb = 0; sb < kSub; sb++)
+#pragma unroll
+                for (int rho = 0; rho < 16; rho++) mx = fmaxf(mx, s_acc[sb][rho]);
+            mx = pair_max(mx);
+            float m_new = fmaxf(m_run, mx);
+            float m_use = m_new == -INFINITY ? 0.f : m_new;
+            float alpha = fast_exp2(m_run - m_use);
+            m_run = m_new;
+            float rs = 0.f;
+            x8 p[kSub][2];
+#pragma unroll
+            for (int sb = 0; sb < kSub; sb++) {
+#pragma unroll
+                for (int rho = 0; rho < 16; rho++) {
+                    s_acc[sb][rho] = fast_exp2(s_acc[sb][rho] - m_use);
+                    rs += s_acc[sb][rho];
+                }
+#pragma unroll
+                for (int c = 0; c < 2; c++) {
+                    floatx4 lo, hi;
+#pragma unroll
+                    for (int u = 0; u < 4; u++) {
+                        lo[u] = s_acc[sb][8 * c + u];
+                        hi[u] = s_acc[sb][8 * c + 4 + u];
+                    }
+                    p[sb][c] = __builtin_bit_cast(x8, narrow8<T>(lo, hi));
+                }
+            }
+            l_run = l_run * alpha + rs;
+            if (__any(alpha != 1.f)) {
+#pragma unroll
+                for (int t = 0; t < kTiles; t++) o_acc[t] *= alpha;
+            }
+            // O^T += V^T P^T, 16 keys per MFMA
+#pragma unroll
+            for (int t = 0; t < kTiles; t++) {
+                const uint16_t* vp = &lds.vt[buf][(32 * t + j) * PV + 8 * g];
+#pragma unroll
+                for (int cc = 0; cc < kKB / 16; cc++) {
+                    x8 vv = __builtin_bit_cast(x8, *reinterpret_cast<const u32x4*>(vp + 16 * cc));
+                    o_acc[t] = Lp<T>::mfma(vv, p[cc / 2][cc % 2], o_acc[t]);
+                }
+            }
+        }
+        if (next < nb) stage.store(lds, buf ^ 1, tid);
+        __syncthreads();
+        buf ^= 1;
+        kb = next;
+    }
+
+    float l = pair_sum(l_run);
+    if (j < nq) {
+        float inv = l > 0.f ? 1.f / l : 0.f;
+        T* op = out + ((size_t)r * n + q0 + j) * inner + h * DH;
+        // O^T reg 4a+u of lane (j, g) in tile t is dim 32t + 8a + 4g + u of query j
+#pragma unroll
+        for (int t = 0; t < kTiles; t++) {
+#pragma unroll
+            for (int a = 0; a < 4; a++) {
+                int e = 32 * t + 8 * a + 4 * g;
+                if (e < DH) {
+                    floatx4 v;
+#pragma unroll
+                    for (int u = 0; u < 4; u++) v[u] = o_acc[t][4 * a + u] * inv;
+                    *reinterpret_cast<u32x2*>(op + e) = narrow4<T>(v);
+                }
+            }
+        }
+    }
+}
+
+constexpr int kNW = 4;  // waves per workgroup
+
+template <typename T, int DH>
+hipError_t launch_lp(const void* qkv, void* out, const int32_t* live, const float* table, int rows, int n, int heads,
+                     int inner, hipStream_t stream) {
+    int tiles = (n + kQ - 1) / kQ;
+    int qgroups = (tiles + kNW - 1) / kNW;
+    uint64_t grid = (uint64_t)rows * heads * qgroups;
+    if (table) {
+        hipLaunchKernelGGL((c2_time_attention_lp<T, DH, kNW, true>), dim3((uint32_t)grid), dim3(kNW * kWave), 0,
+                           stream, (const T*)qkv, (T*)out, live, table, rows, n, heads, inner, qgroups);
+    } else {
+        hipLaunchKernelGGL((c2_time_attention_lp<T, DH, kNW, false>), dim3((uint32_t)grid), dim3(kNW * kWave), 0,
+                           stream, (const T*)qkv, (T*)out, live, table, rows, n, heads, inner, qgroups);
+    }
+    return hipGetLastError();
+}
+
+template <typename T>
+hipError_t dispatch_lp(const void* qkv, void* out, const int32_t* live, const float* table, int rows, int n, int heads,
+                       int dh, int inner, hipStream_t stream) {
+    switch (dh) {
+        case 16: return launch_lp<T, 16>(qkv, out, live, table, rows, n, heads, inner, stream);
+        case 32: return launch_lp<T, 32>(qkv, out, live, table, rows, n, heads, inner, stream);
+        case 48: return launch_lp<T, 48>(qkv, out, live, table, rows, n, heads, inner, stream);
+        case 64: return launch_lp<T, 64>(qkv, out, live, table, rows, n, heads, inner, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace
+
+hipError_t c2_time_attention_lp_launch(const void* qkv, void* out, const int32_t* live, const float* table, int rows,
+                                       int n, int heads, int dh, int inner, bool fp16, hipStream_t stream) {
+    return fp16 ? dispatch_lp<_Float16>(qkv, out, live, table, rows, n, heads, dh, inner, stream)
+                : dispatch_lp<__bf16>(qkv, out, live, table, rows, n, heads, dh, inner, stream);
+}
+
+}  // namespace jc

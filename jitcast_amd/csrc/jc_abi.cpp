@@ -239,7 +239,10 @@ int jc_c2_time_attention(jc_ctx* ctx, const void* qkv, void* out, const int32_t*
         e = jc::c2_time_attention_f32_launch((const float*)qkv, (float*)out, live, table, rows, n, heads, dh, inner,
                                              ctx->stream);
     } else {
-        return fail(JC_EUNSUPPORTED, "%s: dtype %d is not built yet", W, dtype);
+        if (dh % 16) return fail(JC_EINVAL, "%s: head width %d (bf16/fp16 need a multiple of 16)", W, dh);
+        if (inner % 8) return fail(JC_EINVAL, "%s: inner %d (bf16/fp16 need a multiple of 8)", W, inner);
+        e = jc::c2_time_attention_lp_launch(qkv, out, live, table, rows, n, heads, dh, inner, dtype == JC_F16,
+                                            ctx->stream);
     }
     return e == hipSuccess ? JC_OK : hip_fail(W, e);
 }

@@ -10,6 +10,9 @@ namespace jc {
 hipError_t c2_time_attention_f32_launch(const float* qkv, float* out, const int32_t* live, const float* table,
                                         int rows, int n, int heads, int dh, int inner, hipStream_t stream);
 int c2_time_attention_max_tokens();
+// bf16 (fp16 = false) or fp16 qkv/out, fp32 accumulation; dh a multiple of 16, at most 64
+hipError_t c2_time_attention_lp_launch(const void* qkv, void* out, const int32_t* live, const float* table, int rows,
+                                       int n, int heads, int dh, int inner, bool fp16, hipStream_t stream);
 hipError_t c2_group_attention_f32_launch(const float* qkv, float* out, const int32_t* live, const int32_t* gs,
                                          const int32_t* ge, int rows, int n, int heads, int dh, int inner,
                                          hipStream_t stream);

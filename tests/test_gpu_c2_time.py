@@ -1,6 +1,7 @@
 """GPU parity of the fused Chronos-2 time attention against the C oracle (through the C ABI).
 
-Bar: max relative error (the reference's metric) <= 1e-4 for fp32.
+Bar: max relative error (the reference's metric) <= 1e-4 for fp32 and <= 2e-2 for bf16/fp16 (qkv
+rounded to the storage type, compared with the fp32 oracle on the unrounded qkv).
 """
 import numpy as np
 import pytest
@@ -11,6 +12,8 @@ from tests import brute, cases
 
 pytestmark = pytest.mark.gpu
 TOL_F32 = 1e-4
+TOL_LP = 2e-2
+LP_DTYPES = {"bf16": torch.bfloat16, "fp16": torch.float16}
 
 
 def _run(qkv, live, rows, n, heads, dh, inner, table=True, dtype=torch.float32):
@@ -60,6 +63,71 @@ def test_fp32_matches_oracle(gpu, oracle, rows, n, heads, dh, inner, kind):
     got, exp = got[:, : heads * dh], exp[:, : heads * dh]
     assert np.isfinite(got).all()
     assert oracle.rel_max_error(got, exp) <= TOL_F32
+
+
+LP_CASES = [c for c in CASES if c[3] % 16 == 0 and c[4] % 8 == 0] + [
+    (2, 513, 2, 64, 128, "pad"),
+    (1, 1030, 1, 64, 64, "random"),
+]
+
+
+@pytest.mark.parametrize("dt", sorted(LP_DTYPES))
+@pytest.mark.parametrize("rows,n,heads,dh,inner,kind", LP_CASES)
+def test_lowp_matches_oracle(gpu, oracle, rows, n, heads, dh, inner, kind, dt):
+    print(f"case {dt} rows={rows} n={n} heads={heads} dh={dh} inner={inner} {kind}", flush=True)
+    qkv = cases.qkv(53, rows * n, inner, std=0.554)
+    live = _live(kind, 53, rows, n)
+    got = _run(qkv, live, rows, n, heads, dh, inner, dtype=LP_DTYPES[dt])[:, : heads * dh]
+    assert np.isfinite(got).all()
+    exp = oracle.c2_time_attention(qkv, live, rows, n, heads, dh, inner)[:, : heads * dh]
+    err = oracle.rel_max_error(got, exp)
+    # the kernel's own error: the oracle on the same rounded inputs
+    rounded = torch.from_numpy(qkv).to(LP_DTYPES[dt]).float().numpy()
+    own = oracle.rel_max_error(got, oracle.c2_time_attention(rounded, live, rows, n, heads, dh, inner)[:, : heads * dh])
+    print(f"  rel err {err:.3e} (vs rounded inputs {own:.3e})", flush=True)
+    assert err <= TOL_LP
+    assert own <= TOL_LP / 2
+
+
+@pytest.mark.parametrize("dt", sorted(LP_DTYPES))
+def test_lowp_one_live_key_returns_its_value(gpu, dt):
+    rows, n, heads, dh, inner = 2, 70, 2, 64, 128
+    qkv = cases.qkv(31, rows * n, inner)
+    live = np.zeros((rows, n), np.int32)
+    live[0, 3] = 1
+    live[1, 69] = 1
+    got = _run(qkv, live, rows, n, heads, dh, inner, dtype=LP_DTYPES[dt]).reshape(rows, n, inner)
+    v = torch.from_numpy(qkv).to(LP_DTYPES[dt]).float().numpy().reshape(rows, n, 3 * inner)[:, :, 2 * inner:]
+    # softmax of one key is exactly 1: the output is that key's v, bit for bit in the storage type
+    np.testing.assert_array_equal(got[0], np.broadcast_to(v[0, 3], (n, inner)))
+    np.testing.assert_array_equal(got[1], np.broadcast_to(v[1, 69], (n, inner)))
+
+
+@pytest.mark.parametrize("dt", sorted(LP_DTYPES))
+def test_lowp_no_live_key_gives_zeros(gpu, dt):
+    rows, n, heads, dh, inner = 3, 40, 2, 64, 128
+    qkv = cases.qkv(29, rows * n, inner)
+    live = cases.left_pad_live(29, rows, n, 10)
+    live[1] = 0
+    got = _run(qkv, live, rows, n, heads, dh, inner, dtype=LP_DTYPES[dt]).reshape(rows, n, inner)
+    assert not np.any(got[1])
+    assert np.isfinite(got).all()
+
+
+def test_bf16_config1_shape_subset_matches_oracle(gpu, oracle):
+    """Config 1-bf16: the config-1 inputs (12 series) with qkv rounded to bf16, against the fp32 oracle."""
+    from jitcast_amd import synthetic
+
+    case = synthetic.c2_time_config1(rows=12, device="cuda")
+    q16 = case.qkv.to(torch.bfloat16)
+    out = torch.empty(case.rows * case.n, case.inner, device="cuda", dtype=torch.bfloat16)
+    chronos2.time_attention(q16, out, case.live, case.rows, case.n, case.heads, case.dh, case.inner, case.table)
+    torch.cuda.synchronize()
+    exp = oracle.c2_time_attention(case.qkv.cpu().numpy(), case.live.cpu().numpy(), case.rows, case.n, case.heads,
+                                   case.dh, case.inner)
+    err = oracle.rel_max_error(out.float().cpu().numpy(), exp)
+    print(f"config-1 bf16 subset rel err {err:.3e}", flush=True)
+    assert err <= TOL_LP
 
 
 def test_fp32_no_live_key_gives_zeros(gpu, oracle):
