@@ -122,6 +122,10 @@ struct LpStage {
     u32x2 v[kPerV][4];
     uint32_t off_k[kPerK], off_t[kPerK], off_v[kPerV];
 
+    // V items start 256 threads after K items (mod NT), so a workgroup of more than 256 threads
+    // spreads the two kinds of work over different waves
+    static __device__ __forceinline__ int vtid(int tid) { return NT > 256 ? (tid + 256) % NT : tid; }
+
     __device__ __forceinline__ void init(int tid, int inner) {
         const uint32_t stride = 3u * inner * 2u;
 #pragma unroll
@@ -133,7 +137,7 @@ struct LpStage {
         }
 #pragma unroll
         for (int i = 0; i < kPerV; i++) {
-            int it = tid + i * NT;
+            int it = vtid(tid) + i * NT;
             int kq = it / (DH / 4), e4 = it % (DH / 4);
             off_v[i] = 4 * kq * stride + inner * 2 + e4 * 8;
         }
@@ -155,7 +159,7 @@ struct LpStage {
         }
 #pragma unroll
         for (int i = 0; i < kPerV; i++) {
-            if (kItemsV % NT != 0 && tid + i * NT >= kItemsV) break;
+            if (kItemsV % NT != 0 && vtid(tid) + i * NT >= kItemsV) break;
 #pragma unroll
             for (int u = 0; u < 4; u++)
                 v[i][u] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rk, off_v[i] + u * stride, 0, 0));
@@ -183,7 +187,7 @@ struct LpStage {
         }
 #pragma unroll
         for (int i = 0; i < kPerV; i++) {
-            int it = tid + i * NT;
+            int it = vtid(tid) + i * NT;
             if (kItemsV % NT != 0 && it >= kItemsV) break;
             int kq = it / (DH / 4), e4 = it % (DH / 4);
             int pos = vt_pos(4 * kq);
@@ -201,21 +205,70 @@ struct LpStage {
     }
 };
 
+// Encodings of the extra QK^T step (dims 0 and 1 of a 16-dim step, the rest zero):
+//   K' = [bias_k, 1]     bias_k = 0 for a live key, kBigK for a dead one
+//   Q' = [kBigQ, b_m]    b_m = -m: the query's reference max, rounded to T
+// so the MFMA yields s - m for live keys and about -2^100 (bf16) or -2^25 (fp16) for dead ones.
+template <typename T>
+struct Enc;
+template <>
+struct Enc<__bf16> {
+    static constexpr uint32_t kLive = 0x3F800000u;  // (0, 1.0)
+    static constexpr uint32_t kDead = 0x3F80F180u;  // (-2^100, 1.0)
+    static constexpr uint32_t kBigQ = 0x3F80u;      // 1.0
+    static constexpr uint32_t kOnes = 0x3F803F80u;  // (1.0, 1.0)
+    static constexpr float kMax = 3.0e38f;
+    static __device__ __forceinline__ float dot2(uint32_t p, float acc) {
+        typedef __bf16 t2 __attribute__((ext_vector_type(2)));
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(t2, p), __builtin_bit_cast(t2, kOnes), acc, false);
+    }
+};
+template <>
+struct Enc<_Float16> {
+    static constexpr uint32_t kLive = 0x3C000000u;  // (0, 1.0)
+    static constexpr uint32_t kDead = 0x3C00F800u;  // (-32768, 1.0); times kBigQ = 1024: -2^25
+    static constexpr uint32_t kBigQ = 0x6400u;      // 1024.0
+    static constexpr uint32_t kOnes = 0x3C003C00u;
+    static constexpr float kMax = 65504.f;
+    static __device__ __forceinline__ float dot2(uint32_t p, float acc) {
+        typedef _Float16 t2 __attribute__((ext_vector_type(2)));
+        return __builtin_amdgcn_fdot2(__builtin_bit_cast(t2, p), __builtin_bit_cast(t2, kOnes), acc, false);
+    }
+};
+
+template <typename T>
+__device__ __forceinline__ uint32_t to_bits(float x) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (T)x);
+}
+template <typename T>
+__device__ __forceinline__ float from_bits(uint32_t b) {
+    return (float)__builtin_bit_cast(T, (uint16_t)b);
+}
+
+// Online softmax without a per-element max or subtraction on the common path: scores arrive
+// already relative to the query's reference max m (the extra MFMA step), P = exp2(S) is rounded to
+// T, and the block's row sum comes from v_dot2 over the packed P (the same rounded values the PV
+// MFMA consumes). Only when some query's block sum leaves [2^-16, 2^16] (first block) or exceeds
+// 2^16 (later blocks) does the wave take the slow path: the exact block max, a new reference
+// rounded to T, P recomputed, and the O/l rescale. Bounding P by 2^16 keeps every sum finite.
+constexpr float kSumHi = 65536.f;
+constexpr float kSumLo = 1.0f / 65536.f;
+
 template <typename T, int DH, int NW, bool ROPE>
-__global__ __launch_bounds__(NW * kWave) void c2_time_attention_lp(const T* __restrict__ qkv, T* __restrict__ out,
+__global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(NW >= 4 ? 3 : 2))) void c2_time_attention_lp(const T* __restrict__ qkv, T* __restrict__ out,
                                                                     const int32_t* __restrict__ live,
                                                                     const float* __restrict__ table, int rows, int n,
                                                                     int heads, int inner, int qgroups) {
     static_assert(DH % 16 == 0 && DH <= 64, "head width");
     constexpr int NT = NW * kWave;
     constexpr int kHalf = DH / 2;
-    constexpr int kSteps = DH / 16;  // QK^T MFMA steps (16 dims each)
+    constexpr int kSteps = DH / 16;  // QK^T MFMA steps (16 dims each), plus the bias step
     constexpr int kTiles = LpLds<DH>::kTiles;
     constexpr int kSub = kKB / 32;   // 32-key S^T tiles per block
     constexpr int PK = LpLds<DH>::kPitchK, PV = LpLds<DH>::kPitchV;
     typedef typename Lp<T>::x8 x8;
+    typedef Enc<T> E;
     __shared__ LpLds<DH> lds;
-    __shared__ int first_live;
 
     const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
     const int j = lane % 32, g = lane / 32;
@@ -226,84 +279,94 @@ __global__ __launch_bounds__(NW * kWave) void c2_time_attention_lp(const T* __re
     const int h = bh % heads, r = bh / heads;
     const int32_t* lrow = live + (size_t)r * n;
 
+    // The prologue has two load latencies, not four: the wave's raw queries (and their RoPE partner
+    // chunks and table rows) are requested first, so they arrive while the live row is scanned.
+    // Lane (j, g) of step s holds dims 16s+8g..+7 of query q0+j.
+    const int q0 = (qg * NW + wave) * kQ;
+    const int nq = min(max(n - q0, 0), kQ);
+    u32x4 q_own[kSteps], q_par[kSteps];
+    floatx4 t_c0[kSteps], t_c1[kSteps], t_s0[kSteps], t_s1[kSteps];
+    if (j < nq) {
+        const T* qp = qkv + ((size_t)r * n + q0 + j) * 3 * inner + h * DH;
+#pragma unroll
+        for (int s = 0; s < kSteps; s++) {
+            const int d0 = 16 * s + 8 * g;
+            const int e0 = d0 < kHalf ? d0 : d0 - kHalf;  // the rotation partner is half a head away
+            q_own[s] = *reinterpret_cast<const u32x4*>(qp + d0);
+            if (ROPE) {
+                q_par[s] = *reinterpret_cast<const u32x4*>(qp + (d0 < kHalf ? d0 + kHalf : e0));
+                const float* tp = table + (size_t)(q0 + j) * DH + e0;
+                t_c0[s] = *reinterpret_cast<const floatx4*>(tp);
+                t_c1[s] = *reinterpret_cast<const floatx4*>(tp + 4);
+                t_s0[s] = *reinterpret_cast<const floatx4*>(tp + kHalf);
+                t_s1[s] = *reinterpret_cast<const floatx4*>(tp + kHalf + 4);
+            }
+        }
+    }
+
     // padded V^T rows (DH not a multiple of 32) feed only discarded output dims; zero them once
     if (DH % 32 != 0) {
         for (int i = tid; i < 2 * kTiles * 32 * PV; i += NT) (&lds.vt[0][0])[i] = 0;
     }
-    if (tid == 0) first_live = n;
-    __syncthreads();
-    for (int base = wave * kWave; base < n; base += NT) {
-        int k = base + lane;
+    // live bitmask of every 64-key block of the row (blocks aligned to 64; n <= 4096 gives <= 64)
+    const int nblk = (n + kKB - 1) / kKB;
+    for (int b = wave; b < nblk; b += NW) {
+        int k = b * kKB + lane;
         uint64_t bits = __ballot(k < n && lrow[k] != 0);
-        if (bits && lane == 0) atomicMin(&first_live, base + (int)__builtin_ctzll(bits));
+        if (lane == 0) lds.mask[b] = bits;
     }
     __syncthreads();
-    const int kstart = first_live;
-    const int nb = (n - kstart + kKB - 1) / kKB;
-    for (int kb = wave; kb * kKB < n - kstart; kb += NW) {
-        int k = kstart + kb * kKB + lane;
-        uint64_t bits = __ballot(k < n && lrow[k] != 0);
-        if (lane == 0) lds.mask[kb] = bits;
-    }
+    // blocks with a live key (bit b = block b), the same in every wave
+    const uint64_t live_blocks = __ballot(lane < nblk && lds.mask[lane] != 0);
+    auto next_block = [&](int after) {
+        uint64_t rest = after + 1 >= 64 ? 0ull : live_blocks & (~0ull << (after + 1));
+        return rest ? (int)__builtin_ctzll(rest) : nblk;
+    };
 
-    // Q in registers: lane (j, g) holds dims 16s+8g..+7 of query q0+j, rotated, scaled by log2(e),
-    // rounded to T (the B operand of step s)
-    const int q0 = (qg * NW + wave) * kQ;
-    const int nq = min(max(n - q0, 0), kQ);
+    // Q operands: rotated, scaled by log2(e), rounded to T
     x8 qreg[kSteps];
-    {
-        const int q = q0 + j;
 #pragma unroll
-        for (int s = 0; s < kSteps; s++) {
-            floatx4 lo = floatx4{0.f, 0.f, 0.f, 0.f}, hi = lo;
-            if (j < nq) {
-                const int d0 = 16 * s + 8 * g;
-                const T* qp = qkv + ((size_t)r * n + q) * 3 * inner + h * DH;
-                widen8<T>(*reinterpret_cast<const u32x4*>(qp + d0), lo, hi);
-                if (ROPE) {
-                    // the rotation partner of dims d0..d0+7 is the chunk half a head away
-                    const int e0 = d0 < kHalf ? d0 : d0 - kHalf;
-                    floatx4 plo, phi;
-                    widen8<T>(*reinterpret_cast<const u32x4*>(qp + (d0 < kHalf ? d0 + kHalf : e0)), plo, phi);
-                    const float* tp = table + (size_t)q * DH + e0;
-                    floatx4 c0 = *reinterpret_cast<const floatx4*>(tp), c1 = *reinterpret_cast<const floatx4*>(tp + 4);
-                    floatx4 s0 = *reinterpret_cast<const floatx4*>(tp + kHalf);
-                    floatx4 s1 = *reinterpret_cast<const floatx4*>(tp + kHalf + 4);
-                    if (d0 < kHalf) {
-                        lo = lo * c0 - plo * s0;
-                        hi = hi * c1 - phi * s1;
-                    } else {
-                        lo = lo * c0 + plo * s0;
-                        hi = hi * c1 + phi * s1;
-                    }
+    for (int s = 0; s < kSteps; s++) {
+        floatx4 lo = floatx4{0.f, 0.f, 0.f, 0.f}, hi = lo;
+        if (j < nq) {
+            widen8<T>(q_own[s], lo, hi);
+            if (ROPE) {
+                floatx4 plo, phi;
+                widen8<T>(q_par[s], plo, phi);
+                if (16 * s + 8 * g < kHalf) {
+                    lo = lo * t_c0[s] - plo * t_s0[s];
+                    hi = hi * t_c1[s] - phi * t_s1[s];
+                } else {
+                    lo = lo * t_c0[s] + plo * t_s0[s];
+                    hi = hi * t_c1[s] + phi * t_s1[s];
                 }
-                lo *= kLog2e;
-                hi *= kLog2e;
             }
-            qreg[s] = __builtin_bit_cast(x8, narrow8<T>(lo, hi));
+            lo *= kLog2e;
+            hi *= kLog2e;
         }
+        qreg[s] = __builtin_bit_cast(x8, narrow8<T>(lo, hi));
     }
-    __syncthreads();
 
     const size_t row0 = (size_t)r * n;
     const uint32_t stride_b = 3u * inner * 2u;
-    auto rk_at = [&](int kb) {
-        int k = kstart + kb * kKB;
+    // resources over k (and v) of (row, head) from the block's first key to the end of the row, and
+    // over the table rows from that key: keys past n read as zero (and are dead in the mask)
+    auto rk_at = [&](int b) {
+        int k = b * kKB;
         const T* p = qkv + (row0 + k) * 3 * inner + inner + h * DH;
         uint32_t bytes = (uint32_t)(n - k) * stride_b - (uint32_t)(inner + h * DH) * 2u;
         return make_rsrc(p, bytes);
     };
-    auto rt_at = [&](int kb) {
-        int k = kstart + kb * kKB;
+    auto rt_at = [&](int b) {
+        int k = b * kKB;
         return make_rsrc(table + (size_t)k * DH, (uint32_t)((n - k) * DH * 4));
     };
 
-    int kb = 0;
-    while (kb < nb && lds.mask[kb] == 0) kb++;
+    int kb = next_block(-1);
 
     LpStage<T, DH, NT, ROPE> stage;
     stage.init(tid, inner);
-    if (kb < nb) {
+    if (kb < nblk) {
         stage.load(rk_at(kb), ROPE ? rt_at(kb) : rk_at(kb), tid, inner);
         stage.store(lds, 0, tid);
     }
@@ -312,18 +375,23 @@ __global__ __launch_bounds__(NW * kWave) void c2_time_attention_lp(const T* __re
     floatx16 o_acc[kTiles];
 #pragma unroll
     for (int t = 0; t < kTiles; t++) o_acc[t] = floatx16{0};
-    float m_run = -INFINITY, l_run = 0.f;
+    // softmax state of query j (equal in lanes j and j+32): the reference max m_tot, the part of it
+    // the MFMA subtracts (m_mfma = -b_m exactly), their difference (non-zero only when -m_tot does
+    // not fit T), and the running sum l relative to m_tot
+    float m_tot = 0.f, m_mfma = 0.f, resid = 0.f, l_run = 0.f;
+    bool have_ref = false, any_resid = false;
+    uint32_t qx0 = g == 0 ? E::kBigQ : 0u;  // Q' dims 0,1 = (kBigQ, b_m = 0)
     int buf = 0;
-    // settle the prologue loads here, not inside every iteration
     __builtin_amdgcn_s_waitcnt(0);
 
-    while (kb < nb) {
-        int next = kb + 1;
-        while (next < nb && lds.mask[next] == 0) next++;
-        if (next < nb) stage.load(rk_at(next), ROPE ? rt_at(next) : rk_at(next), tid, inner);
+    while (kb < nblk) {
+        const int next = next_block(kb);
+        if (next < nblk) stage.load(rk_at(next), ROPE ? rt_at(next) : rk_at(next), tid, inner);
         __builtin_amdgcn_sched_barrier(0);
 
         if (nq > 0) {
+            const uint64_t km = lds.mask[kb];
+            const x8 qx = __builtin_bit_cast(x8, u32x4{qx0, 0u, 0u, 0u});
             floatx16 s_acc[kSub];
 #pragma unroll
             for (int sb = 0; sb < kSub; sb++) {
@@ -334,54 +402,85 @@ __global__ __launch_bounds__(NW * kWave) void c2_time_attention_lp(const T* __re
                     x8 kv = __builtin_bit_cast(x8, *reinterpret_cast<const u32x4*>(kp + 16 * s));
                     s_acc[sb] = Lp<T>::mfma(kv, qreg[s], s_acc[sb]);
                 }
+                // the bias step: A row i = key 32sb + i
+                const uint32_t kx0 = g == 0 ? (((km >> (32 * sb + j)) & 1ull) ? E::kLive : E::kDead) : 0u;
+                s_acc[sb] = Lp<T>::mfma(__builtin_bit_cast(x8, u32x4{kx0, 0u, 0u, 0u}), qx, s_acc[sb]);
             }
             // reg rho of tile sb in lane (j, g) holds key 32sb + 8*(rho/4) + 4g + rho%4 of the block
-            uint64_t km = lds.mask[kb];
-            if (km != ~0ull) {
-#pragma unroll
-                for (int sb = 0; sb < kSub; sb++) {
-#pragma unroll
-                    for (int rho = 0; rho < 16; rho++) {
-                        int bit = 32 * sb + 8 * (rho / 4) + 4 * g + (rho % 4);
-                        if (!((km >> bit) & 1ull)) s_acc[sb][rho] = -INFINITY;
-                    }
-                }
-            }
-            float mx = s_acc[0][0];
-#pragma unroll
-            for (int sb = 0; sb < kSub; sb++)
-#pragma unroll
-                for (int rho = 0; rho < 16; rho++) mx = fmaxf(mx, s_acc[sb][rho]);
-            mx = pair_max(mx);
-            float m_new = fmaxf(m_run, mx);
-            float m_use = m_new == -INFINITY ? 0.f : m_new;
-            float alpha = fast_exp2(m_run - m_use);
-            m_run = m_new;
-            float rs = 0.f;
             x8 p[kSub][2];
+            auto exps = [&](float shift) {
 #pragma unroll
-            for (int sb = 0; sb < kSub; sb++) {
+                for (int sb = 0; sb < kSub; sb++)
 #pragma unroll
-                for (int rho = 0; rho < 16; rho++) {
-                    s_acc[sb][rho] = fast_exp2(s_acc[sb][rho] - m_use);
-                    rs += s_acc[sb][rho];
-                }
+                    for (int c = 0; c < 2; c++) {
+                        floatx4 lo, hi;
 #pragma unroll
-                for (int c = 0; c < 2; c++) {
-                    floatx4 lo, hi;
-#pragma unroll
-                    for (int u = 0; u < 4; u++) {
-                        lo[u] = s_acc[sb][8 * c + u];
-                        hi[u] = s_acc[sb][8 * c + 4 + u];
+                        for (int u = 0; u < 4; u++) {
+                            lo[u] = fast_exp2(s_acc[sb][8 * c + u] - shift);
+                            hi[u] = fast_exp2(s_acc[sb][8 * c + 4 + u] - shift);
+                        }
+                        p[sb][c] = __builtin_bit_cast(x8, narrow8<T>(lo, hi));
                     }
-                    p[sb][c] = __builtin_bit_cast(x8, narrow8<T>(lo, hi));
-                }
-            }
-            l_run = l_run * alpha + rs;
-            if (__any(alpha != 1.f)) {
+            };
+            auto block_sum = [&]() {
+                float acc = 0.f;
 #pragma unroll
-                for (int t = 0; t < kTiles; t++) o_acc[t] *= alpha;
+                for (int sb = 0; sb < kSub; sb++)
+#pragma unroll
+                    for (int c = 0; c < 2; c++) {
+                        u32x4 w = __builtin_bit_cast(u32x4, p[sb][c]);
+#pragma unroll
+                        for (int d = 0; d < 4; d++) acc = E::dot2(w[d], acc);
+                    }
+                return pair_sum(acc);
+            };
+            if (!any_resid) {
+#pragma unroll
+                for (int sb = 0; sb < kSub; sb++)
+#pragma unroll
+                    for (int c = 0; c < 2; c++) {
+                        floatx4 lo, hi;
+#pragma unroll
+                        for (int u = 0; u < 4; u++) {
+                            lo[u] = fast_exp2(s_acc[sb][8 * c + u]);
+                            hi[u] = fast_exp2(s_acc[sb][8 * c + 4 + u]);
+                        }
+                        p[sb][c] = __builtin_bit_cast(x8, narrow8<T>(lo, hi));
+                    }
+            } else {
+                exps(resid);
             }
+            float lb = block_sum();
+            const bool bad = !(lb <= kSumHi) || (!have_ref && !(lb >= kSumLo));
+            if (__any(bad)) {
+                // the exact block max (relative to m_mfma), a new reference rounded to T
+                float mx = s_acc[0][0];
+#pragma unroll
+                for (int sb = 0; sb < kSub; sb++)
+#pragma unroll
+                    for (int rho = 0; rho < 16; rho++) mx = fmaxf(mx, s_acc[sb][rho]);
+                mx = pair_max(mx);
+                const float s_max = m_mfma + mx;
+                float m_new = have_ref ? fmaxf(m_tot, s_max) : s_max;
+                const uint32_t bm = to_bits<T>(fminf(fmaxf(-m_new, -E::kMax), E::kMax));
+                const float m_enc = -from_bits<T>(bm);
+                if (fabsf(m_new) <= E::kMax) m_new = m_enc;  // keep the reference exactly encodable
+                exps(m_new - m_mfma);
+                lb = block_sum();
+                if (have_ref) {
+                    const float alpha = fast_exp2(m_tot - m_new);
+#pragma unroll
+                    for (int t = 0; t < kTiles; t++) o_acc[t] *= alpha;
+                    l_run *= alpha;
+                }
+                m_tot = m_new;
+                m_mfma = m_enc;
+                resid = m_tot - m_mfma;
+                any_resid = __any(resid != 0.f);
+                qx0 = g == 0 ? (E::kBigQ | (bm << 16)) : 0u;
+            }
+            l_run += lb;
+            have_ref = true;
             // O^T += V^T P^T, 16 keys per MFMA
 #pragma unroll
             for (int t = 0; t < kTiles; t++) {
@@ -393,15 +492,14 @@ __global__ __launch_bounds__(NW * kWave) void c2_time_attention_lp(const T* __re
                 }
             }
         }
-        if (next < nb) stage.store(lds, buf ^ 1, tid);
+        if (next < nblk) stage.store(lds, buf ^ 1, tid);
         __syncthreads();
         buf ^= 1;
         kb = next;
     }
 
-    float l = pair_sum(l_run);
     if (j < nq) {
-        float inv = l > 0.f ? 1.f / l : 0.f;
+        const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
         T* op = out + ((size_t)r * n + q0 + j) * inner + h * DH;
         // O^T reg 4a+u of lane (j, g) in tile t is dim 32t + 8a + 4g + u of query j
 #pragma unroll
@@ -420,22 +518,31 @@ __global__ __launch_bounds__(NW * kWave) void c2_time_attention_lp(const T* __re
     }
 }
 
-constexpr int kNW = 4;  // waves per workgroup
-
-template <typename T, int DH>
-hipError_t launch_lp(const void* qkv, void* out, const int32_t* live, const float* table, int rows, int n, int heads,
-                     int inner, hipStream_t stream) {
+template <typename T, int DH, int NW>
+hipError_t launch_lp_nw(const void* qkv, void* out, const int32_t* live, const float* table, int rows, int n,
+                        int heads, int inner, hipStream_t stream) {
     int tiles = (n + kQ - 1) / kQ;
-    int qgroups = (tiles + kNW - 1) / kNW;
+    int qgroups = (tiles + NW - 1) / NW;
     uint64_t grid = (uint64_t)rows * heads * qgroups;
     if (table) {
-        hipLaunchKernelGGL((c2_time_attention_lp<T, DH, kNW, true>), dim3((uint32_t)grid), dim3(kNW * kWave), 0,
-                           stream, (const T*)qkv, (T*)out, live, table, rows, n, heads, inner, qgroups);
+        hipLaunchKernelGGL((c2_time_attention_lp<T, DH, NW, true>), dim3((uint32_t)grid), dim3(NW * kWave), 0, stream,
+                           (const T*)qkv, (T*)out, live, table, rows, n, heads, inner, qgroups);
     } else {
-        hipLaunchKernelGGL((c2_time_attention_lp<T, DH, kNW, false>), dim3((uint32_t)grid), dim3(kNW * kWave), 0,
+        hipLaunchKernelGGL((c2_time_attention_lp<T, DH, NW, false>), dim3((uint32_t)grid), dim3(NW * kWave), 0,
                            stream, (const T*)qkv, (T*)out, live, table, rows, n, heads, inner, qgroups);
     }
     return hipGetLastError();
+}
+
+// Waves per workgroup: 4 (2 when the row has at most 2 query tiles). Measured on config 1
+// (n = 513, 17 tiles): 4 waves 0.511 ms, 6 waves 0.634 ms, 8 waves 0.611 ms. The kernel is bound by
+// the latency of each workgroup's prologue and per-block loads; three 4-wave workgroups per CU
+// overlap those better than two 6-wave ones, which outweighs the extra idle query slots.
+template <typename T, int DH>
+hipError_t launch_lp(const void* qkv, void* out, const int32_t* live, const float* table, int rows, int n, int heads,
+                     int inner, hipStream_t stream) {
+    if ((n + kQ - 1) / kQ <= 2) return launch_lp_nw<T, DH, 2>(qkv, out, live, table, rows, n, heads, inner, stream);
+    return launch_lp_nw<T, DH, 4>(qkv, out, live, table, rows, n, heads, inner, stream);
 }
 
 template <typename T>

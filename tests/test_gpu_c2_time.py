@@ -114,6 +114,45 @@ def test_lowp_no_live_key_gives_zeros(gpu, dt):
     assert np.isfinite(got).all()
 
 
+def _lowp_operand_model(qkv_rounded, live, rows, n, heads, dh, inner, tdtype):
+    """float64 attention over the operands the MFMAs actually see: q rotated, scaled by log2(e) and
+    rounded to the storage type; k rotated and rounded; v as stored. Isolates the kernel's softmax
+    logic from operand rounding (which at large score scales dominates any bf16 kernel's error)."""
+    q, k, v = brute.split_qkv(qkv_rounded, rows, n, heads, dh, inner)
+    pos = np.broadcast_to(np.arange(n), (rows, n))
+    inv = brute.inv_freq(dh)
+    l2e = np.float32(1.4426950408889634)
+
+    def rnd(x):
+        return torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(tdtype).double().numpy()
+
+    qr = rnd(brute.rope_float(q, pos, inv) * l2e).transpose(0, 2, 1, 3)
+    kr = rnd(brute.rope_float(k, pos, inv)).transpose(0, 2, 1, 3)
+    s = qr @ kr.transpose(0, 1, 3, 2)  # log2 units
+    s = np.where(live[:, None, None, :] == 1, s, -np.inf)
+    p = np.exp2(s - s.max(-1, keepdims=True))
+    o = (p / p.sum(-1, keepdims=True)) @ v.astype(np.float64).transpose(0, 2, 1, 3)
+    return o.transpose(0, 2, 1, 3).reshape(rows * n, heads * dh)
+
+
+@pytest.mark.parametrize("dt", sorted(LP_DTYPES))
+@pytest.mark.parametrize("std,n", [(2.5, 300), (6.0, 129), (0.05, 200)])
+def test_lowp_extreme_score_scales(gpu, oracle, dt, std, n):
+    """Large scores move the block max by tens of log2 units between blocks (the rescaling slow
+    path on most blocks); tiny scores keep every block on the fast path. Checked against the
+    float64 model of the rounded MFMA operands."""
+    rows, heads, dh, inner = 2, 2, 64, 128
+    qkv = cases.qkv(59, rows * n, inner, std=std)
+    live = cases.left_pad_live(59, rows, n, n // 3)
+    got = _run(qkv, live, rows, n, heads, dh, inner, dtype=LP_DTYPES[dt])[:, : heads * dh]
+    assert np.isfinite(got).all()
+    rounded = torch.from_numpy(qkv).to(LP_DTYPES[dt]).float().numpy()
+    exp = _lowp_operand_model(rounded, live, rows, n, heads, dh, inner, LP_DTYPES[dt])
+    err = oracle.rel_max_error(got, exp)
+    print(f"  std {std}: rel err vs the operand model {err:.3e}", flush=True)
+    assert err <= TOL_LP / 2
+
+
 def test_bf16_config1_shape_subset_matches_oracle(gpu, oracle):
     """Config 1-bf16: the config-1 inputs (12 series) with qkv rounded to bf16, against the fp32 oracle."""
     from jitcast_amd import synthetic
