@@ -126,6 +126,48 @@ int jc_c2_time_attention(jc_ctx *ctx, const void *qkv, void *out, const int32_t 
 int jc_c2_group_attention(jc_ctx *ctx, const void *qkv, void *out, const int32_t *live, const int32_t *group_start,
                           const int32_t *group_end, int rows, int n, int heads, int dh, int inner, int dtype);
 
+/* ---- Timestral time attention ----------------------------------------------------------------- */
+
+/*
+ * The host-built RoPE table over every position a token can have, (-enc, enc + h): row p holds
+ * cos((float)(p - enc) * invFreq[e]) at e < dh/2 and the sin at dh/2 + e (double cos/sin rounded to
+ * float), invFreq[i] = 1/(float)pow(theta, (float)(2i)/rope_dim) for i < rope_dim/2 and 0 after (those
+ * dims pass through). n = enc + h tokens per row; writes host memory [(enc + n) * dh].
+ * Replaces TimestralForward.Plan.run's table fill (J/timestral/tornado/TimestralForward.java:599-610)
+ * and CpuTimestral.inverseFrequencies (J/timestral/cpu/CpuTimestral.java:107-116).
+ */
+int jc_ts_rope_table(int enc, int n, int dh, int rope_dim, float theta, float *table_host);
+
+/*
+ * Fused RoPE + masked time attention + output gate of one Timestral attention sublayer: scores
+ * q.k/sqrt(dh) under BlockLayout.timeAllowed (encoder query q < enc: keys k < enc with k == q or
+ * (key_valid[r][k] and (k <= q or known[r])); decoder query: valid context keys k < ll and decoder
+ * keys k <= q), RoPE at table row pos[token] for q and k, and out *= sigmoid(gate) when gate is not
+ * NULL.
+ * Replaces TimestralKernels.rope(qkv, pos, table, tokens, heads, dh, d), TimestralKernels.timeAttention(
+ * qkv, out, keyValid, known, rows, enc, ll, n, heads, dh, d) and TimestralKernels.gate(att, g, count)
+ * (J/timestral/tornado/TimestralKernels.java:77-78, 114-115, 573); oracle CpuTimestral.java:150-163,
+ * 190-259; masks BlockLayout.java:209-221.
+ *   qkv, out     device, [rows*n, 3*d] and [rows*n, d] of `dtype` (q|k|v heads-major per token)
+ *   key_valid    device int32 [rows*enc]; known device int32 [rows] or NULL (no known rows)
+ *   pos          device int32 [rows*n]: table row of each token (position + enc), clamped into the
+ *                table's enc + n rows; NULL uses the token index
+ *   rope_table   device [(enc + n), dh] fp32 from jc_ts_rope_table, or NULL when q, k are rotated
+ *   gate         device [rows*n, d] of `dtype`, or NULL (no gate)
+ *   dh           fp32: a multiple of 8, at most 128 (TimestralForward.java:163-166); bf16/fp16: a
+ *                multiple of 16; d >= heads*dh; 0 <= ll <= enc <= n <= 4096
+ */
+int jc_ts_time_attention(jc_ctx *ctx, const void *qkv, void *out, const int32_t *key_valid, const int32_t *known,
+                         const int32_t *pos, const float *rope_table, const void *gate, int rows, int enc, int ll,
+                         int n, int heads, int dh, int d, int dtype);
+
+/*
+ * att[i] *= sigmoid(g[i]) for i < count, in place on device memory of `dtype` (fp32 16-byte aligned,
+ * bf16/fp16 8-byte aligned). Replaces TimestralKernels.gate(att, g, count)
+ * (J/timestral/tornado/TimestralKernels.java:572-578); the attention entry points fuse it.
+ */
+int jc_ts_gate(jc_ctx *ctx, void *att, const void *g, int64_t count, int dtype);
+
 /* ---- host-side layout (the per-call work the reference does in Java before each upload) ------- */
 
 /*

@@ -215,35 +215,126 @@ int jc_c2_rope_table(int n, int dh, float theta, float* table) {
     return JC_OK;
 }
 
+// Checks shared by the time-attention entry points: a valid head width for the dtype, an inner
+// width the rows can be read with, a row short enough for the kernels' per-row state, pointers
+// aligned for 16-byte loads, and 32-bit byte offsets within one row of qkv.
+static int check_time_common(const char* W, const void* qkv, const void* out, const void* table, const void* gate,
+                             int rows, int n, int heads, int dh, int inner, int dtype, int max_dh) {
+    if (rows < 0 || n < 0 || heads < 1) return fail(JC_EINVAL, "%s: bad shape rows=%d n=%d heads=%d", W, rows, n, heads);
+    if (dtype != JC_F32 && dtype != JC_BF16 && dtype != JC_F16) return fail(JC_EINVAL, "%s: dtype %d", W, dtype);
+    const int mult = dtype == JC_F32 ? 8 : 16;
+    if (dh < mult || dh > max_dh || dh % mult)
+        return fail(JC_EINVAL, "%s: head width %d (need a multiple of %d, <= %d)", W, dh, mult, max_dh);
+    const int imult = dtype == JC_F32 ? 4 : 8;
+    if (inner < heads * dh || inner % imult)
+        return fail(JC_EINVAL, "%s: inner %d (need >= heads*dh = %d and a multiple of %d)", W, inner, heads * dh,
+                    imult);
+    if (n > jc::time_attention_max_tokens())
+        return fail(JC_EINVAL, "%s: %d tokens per row (at most %d)", W, n, jc::time_attention_max_tokens());
+    if ((size_t)rows * n == 0) return JC_OK;
+    if (!qkv || !out) return fail(JC_EINVAL, "%s: null device pointer", W);
+    if (!aligned16(qkv) || !aligned16(out) || (table && !aligned16(table)) || (gate && !aligned16(gate)))
+        return fail(JC_EINVAL, "%s: qkv, out, rope_table and gate must be 16-byte aligned", W);
+    if ((uint64_t)rows * heads * ((n + 31) / 32) > 0x7fffffffull) return fail(JC_EINVAL, "%s: grid too large", W);
+    if ((uint64_t)n * 3 * inner * dtype_size(dtype) >= 0x80000000ull)
+        return fail(JC_EINVAL, "%s: one row of qkv (n*3*inner) must stay under 2 GiB", W);
+    return JC_OK;
+}
+
+static int launch_time(jc_ctx* ctx, const char* W, const jc::TimeArgs& a, int dh, bool ts, int dtype) {
+    hipError_t e = dtype == JC_F32 ? jc::time_attention_f32_launch(a, dh, ts, ctx->stream)
+                                   : jc::time_attention_lp_launch(a, dh, ts, dtype == JC_F16, ctx->stream);
+    return e == hipSuccess ? JC_OK : hip_fail(W, e);
+}
+
 int jc_c2_time_attention(jc_ctx* ctx, const void* qkv, void* out, const int32_t* live, const float* table, int rows,
                          int n, int heads, int dh, int inner, int dtype) {
     const char* W = "jc_c2_time_attention";
     int rc = use(ctx, W);
     if (rc) return rc;
-    if (rows < 0 || n < 0 || heads < 1) return fail(JC_EINVAL, "%s: bad shape rows=%d n=%d heads=%d", W, rows, n, heads);
-    if (dh < 8 || dh > 64 || dh % 8) return fail(JC_EINVAL, "%s: head width %d (need a multiple of 8, <= 64)", W, dh);
-    if (inner < heads * dh || inner % 4)
-        return fail(JC_EINVAL, "%s: inner %d (need >= heads*dh = %d and a multiple of 4)", W, inner, heads * dh);
-    if (n > jc::c2_time_attention_max_tokens())
-        return fail(JC_EINVAL, "%s: %d tokens per row (at most %d)", W, n, jc::c2_time_attention_max_tokens());
-    if (dtype != JC_F32 && dtype != JC_BF16 && dtype != JC_F16) return fail(JC_EINVAL, "%s: dtype %d", W, dtype);
-    if ((size_t)rows * n == 0) return JC_OK;
-    if (!qkv || !out || !live) return fail(JC_EINVAL, "%s: null device pointer", W);
-    if (!aligned16(qkv) || !aligned16(out) || (table && !aligned16(table)))
-        return fail(JC_EINVAL, "%s: qkv, out and rope_table must be 16-byte aligned", W);
-    if ((uint64_t)rows * heads * ((n + 127) / 128) > 0x7fffffffull) return fail(JC_EINVAL, "%s: grid too large", W);
-    if ((uint64_t)n * 3 * inner * dtype_size(dtype) >= 0x80000000ull)
-        return fail(JC_EINVAL, "%s: one row of qkv (n*3*inner) must stay under 2 GiB", W);
-    hipError_t e;
-    if (dtype == JC_F32) {
-        e = jc::c2_time_attention_f32_launch((const float*)qkv, (float*)out, live, table, rows, n, heads, dh, inner,
-                                             ctx->stream);
-    } else {
-        if (dh % 16) return fail(JC_EINVAL, "%s: head width %d (bf16/fp16 need a multiple of 16)", W, dh);
-        if (inner % 8) return fail(JC_EINVAL, "%s: inner %d (bf16/fp16 need a multiple of 8)", W, inner);
-        e = jc::c2_time_attention_lp_launch(qkv, out, live, table, rows, n, heads, dh, inner, dtype == JC_F16,
-                                            ctx->stream);
+    rc = check_time_common(W, qkv, out, table, nullptr, rows, n, heads, dh, inner, dtype, 64);
+    if (rc || (size_t)rows * n == 0) return rc;
+    if (!live) return fail(JC_EINVAL, "%s: null live mask", W);
+    jc::TimeArgs a{};
+    a.qkv = qkv;
+    a.out = out;
+    a.valid = live;
+    a.table = table;
+    a.rows = rows;
+    a.n = n;
+    a.heads = heads;
+    a.inner = inner;
+    a.enc = n;
+    a.ll = n;
+    a.table_rows = n;
+    a.qscale = 1.4426950408889634f;  // unscaled scores, exp via exp2
+    return launch_time(ctx, W, a, dh, false, dtype);
+}
+
+int jc_ts_rope_table(int enc, int n, int dh, int rope_dim, float theta, float* table) {
+    if (enc < 0 || n < enc || dh < 2 || dh % 2 || rope_dim < 2 || rope_dim % 2 || rope_dim > dh || !table ||
+        !(theta > 0.f))
+        return fail(JC_EINVAL, "jc_ts_rope_table: bad arguments (enc=%d n=%d dh=%d rope_dim=%d theta=%g)", enc, n, dh,
+                    rope_dim, (double)theta);
+    const int half = dh / 2;
+    std::vector<float> inv(half, 0.f);
+    for (int i = 0; i < rope_dim / 2; i++) {
+        float ex = (float)(2 * i) / (float)rope_dim;
+        inv[i] = 1.0f / (float)std::pow((double)theta, (double)ex);
     }
+    for (int p = 0; p < enc + n; p++) {
+        const float position = (float)(p - enc);
+        for (int e = 0; e < half; e++) {
+            const float ang = position * inv[e];
+            table[(size_t)p * dh + e] = (float)std::cos((double)ang);
+            table[(size_t)p * dh + half + e] = (float)std::sin((double)ang);
+        }
+    }
+    return JC_OK;
+}
+
+int jc_ts_time_attention(jc_ctx* ctx, const void* qkv, void* out, const int32_t* key_valid, const int32_t* known,
+                         const int32_t* pos, const float* table, const void* gate, int rows, int enc, int ll, int n,
+                         int heads, int dh, int d, int dtype) {
+    const char* W = "jc_ts_time_attention";
+    int rc = use(ctx, W);
+    if (rc) return rc;
+    if (enc < 0 || ll < 0 || ll > enc || n < enc)
+        return fail(JC_EINVAL, "%s: token counts (need 0 <= ll <= enc <= n; got ll=%d enc=%d n=%d)", W, ll, enc, n);
+    rc = check_time_common(W, qkv, out, table, gate, rows, n, heads, dh, d, dtype, 128);
+    if (rc || (size_t)rows * n == 0) return rc;
+    if (enc > 0 && !key_valid) return fail(JC_EINVAL, "%s: null key_valid", W);
+    jc::TimeArgs a{};
+    a.qkv = qkv;
+    a.out = out;
+    a.valid = key_valid;
+    a.known = known;
+    a.pos = pos;
+    a.table = table;
+    a.gate = gate;
+    a.rows = rows;
+    a.n = n;
+    a.heads = heads;
+    a.inner = d;
+    a.enc = enc;
+    a.ll = ll;
+    a.table_rows = enc + n;
+    a.qscale = (float)(1.4426950408889634 / std::sqrt((double)dh));
+    return launch_time(ctx, W, a, dh, true, dtype);
+}
+
+int jc_ts_gate(jc_ctx* ctx, void* att, const void* g, int64_t count, int dtype) {
+    const char* W = "jc_ts_gate";
+    int rc = use(ctx, W);
+    if (rc) return rc;
+    if (count < 0) return fail(JC_EINVAL, "%s: count %lld", W, (long long)count);
+    if (dtype != JC_F32 && dtype != JC_BF16 && dtype != JC_F16) return fail(JC_EINVAL, "%s: dtype %d", W, dtype);
+    if (count == 0) return JC_OK;
+    if (!att || !g) return fail(JC_EINVAL, "%s: null device pointer", W);
+    const size_t align = dtype == JC_F32 ? 16 : 8;
+    if (((uintptr_t)att % align) || ((uintptr_t)g % align))
+        return fail(JC_EINVAL, "%s: att and g must be %zu-byte aligned", W, align);
+    hipError_t e = jc::gate_launch(att, g, (uint64_t)count, dtype, ctx->stream);
     return e == hipSuccess ? JC_OK : hip_fail(W, e);
 }
 

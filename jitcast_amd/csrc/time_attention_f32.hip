@@ -1,0 +1,421 @@
+// Time attention, fused flash-style for gfx950: the FP32 path of Chronos-2 and Timestral.
+//
+// Chronos-2 replaces the per-layer pair Chronos2Kernels.rope + Chronos2Kernels.timeAttention
+// (Chronos2Kernels.java:87-116, 118-464; oracle CpuChronos2.java:175-228, 284-304): unscaled scores
+// over the row's live keys, both directions; zeros when no key is live.
+// Timestral replaces TimestralKernels.rope + timeAttention + gate (TimestralKernels.java:71-100,
+// 102-278, 572-578; oracle CpuTimestral.java:190-259, 156-161): scores scaled by 1/sqrt(dh), the
+// BlockLayout.timeAllowed mask (time_mask.hpp), RoPE at each token's position pos[t] (a row of the
+// host-built table), and the optional sigmoid output gate fused into the epilogue.
+//
+// Layout: qkv [rows*n, 3*inner] (q | k | v, heads-major per token), out [rows*n, inner]. One
+// workgroup = 4 waves = 128 consecutive queries of one (row, head); each wave owns 32 queries.
+// Keys stream through LDS in blocks of KB, double-buffered; blocks no query of the workgroup can
+// see are skipped, and a block no query of a wave can see costs that wave nothing but the barrier.
+//
+// MFMA mapping (v_mfma_f32_32x32x2_f32, 64 flops/clk/SIMD):
+//   S^T[key][q] = K Q^T   A = K  (lane i+32kk: K[key i][kk*DHP/2 + s]),  B = Q (same dim map)
+//   O^T[e][q]  += V^T P^T A = V^T (lane i+32kk: V[key(kk,c)][e]),        B = P straight from S^T
+// DHP is the head width padded to a power of two; the real dh (a multiple of 8) fills the first
+// dh/2 dims of each half of the padded Q/K layout, so the RoPE pair (e, e+dh/2) sits in the two
+// lane halves of one step. The accumulator layout of S^T is exactly the B-operand layout P^T needs,
+// so P never leaves registers. One query's softmax state lives in lanes j and j+32.
+//
+// K/V/table prefetch uses buffer loads; keys past the end of the row fall outside the resource and
+// read as 0 (and are masked), so the load path has no per-lane bounds branches.
+#include "jc_common.hpp"
+#include "jc_kernels.hpp"
+#include "time_mask.hpp"
+
+#include <cstdlib>
+
+namespace jc {
+namespace {
+
+constexpr int kQ = 32;        // queries per wave
+constexpr int kWaves = 4;     // waves per workgroup
+constexpr int kThreads = kWaves * kWave;
+constexpr int kMaxTokens = 4096;
+constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer, 32-bit data format (gfx9 family)
+
+template <int DHP, int KB, bool TS>
+struct F32Lds {
+    static constexpr int kPitchK = DHP + 4;         // floats per key row of K
+    static constexpr int kTiles = (DHP + 31) / 32;  // 32-dim output tiles
+    static constexpr int kPitchV = KB + 4;          // floats per dim row of V^T
+    float k[2][KB * kPitchK];
+    float vt[2][kTiles * 32 * kPitchV];
+    uint64_t mask[kMaxTokens / kMaskBlock];  // per 64-key word: key validity bits
+    int32_t pos[TS ? kMaxTokens : 1];       // table row of every token of the row (Timestral)
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, (int)kRsrcWord3);
+}
+
+// One KB-key block of K (rotated at store) and V for (row, head), staged through registers:
+// item `it` covers key it / (dh/8) and dims e..e+3 of each half, e = 4 * (it % (dh/8)).
+template <int DHP, int KB, bool ROPE, bool TS>
+struct KvStage {
+    static constexpr int kMaxItems = KB * DHP / 8;
+    static constexpr int kPer = (kMaxItems + kThreads - 1) / kThreads;
+    floatx4 k0[kPer], k1[kPer], v0[kPer], v1[kPer], c[kPer], s[kPer];
+    uint32_t off_kv[kPer], off_tab[kPer];  // loop-invariant byte offsets
+    int key[kPer], e[kPer];
+    int items, half;
+
+    __device__ __forceinline__ void init(int tid, int inner, int dh) {
+        half = dh / 2;
+        const int quads = dh / 8;
+        items = KB * quads;
+#pragma unroll
+        for (int i = 0; i < kPer; i++) {
+            int it = tid + i * kThreads;
+            key[i] = it / quads;
+            e[i] = (it % quads) * 4;
+            off_kv[i] = (uint32_t)((key[i] * 3 * inner + e[i]) * 4);
+            off_tab[i] = (uint32_t)((key[i] * dh + e[i]) * 4);
+        }
+    }
+
+    // rk: resource over k of (row, head) from the block's first key k0. rt: over the table rows
+    // from k0 (Chronos-2) or over the whole table (Timestral: row = pos of the key).
+    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rt, const int32_t* pos,
+                                         int kbase, int n, int tid, int inner, int dh) {
+#pragma unroll
+        for (int i = 0; i < kPer; i++) {
+            if (tid + i * kThreads >= items) break;
+            k0[i] = __builtin_amdgcn_raw_buffer_load_b128(rk, off_kv[i], 0, 0);
+            k1[i] = __builtin_amdgcn_raw_buffer_load_b128(rk, off_kv[i] + half * 4, 0, 0);
+            v0[i] = __builtin_amdgcn_raw_buffer_load_b128(rk, off_kv[i] + inner * 4, 0, 0);
+            v1[i] = __builtin_amdgcn_raw_buffer_load_b128(rk, off_kv[i] + inner * 4 + half * 4, 0, 0);
+            if (ROPE) {
+                uint32_t ot = off_tab[i];
+                if (TS) {
+                    const int k = kbase + key[i];
+                    ot = (uint32_t)(((k < n ? pos[k] : 0) * dh + e[i]) * 4);
+                }
+                c[i] = __builtin_amdgcn_raw_buffer_load_b128(rt, ot, 0, 0);
+                s[i] = __builtin_amdgcn_raw_buffer_load_b128(rt, ot + half * 4, 0, 0);
+            }
+        }
+    }
+
+    __device__ __forceinline__ void store(F32Lds<DHP, KB, TS>& lds, int buf, int tid) {
+        constexpr int PK = F32Lds<DHP, KB, TS>::kPitchK, PV = F32Lds<DHP, KB, TS>::kPitchV;
+#pragma unroll
+        for (int i = 0; i < kPer; i++) {
+            if (tid + i * kThreads >= items) break;
+            floatx4 a0 = k0[i], a1 = k1[i];
+            if (ROPE) {
+                a0 = k0[i] * c[i] - k1[i] * s[i];
+                a1 = k1[i] * c[i] + k0[i] * s[i];
+            }
+            float* kr = &lds.k[buf][key[i] * PK];
+            *reinterpret_cast<floatx4*>(kr + e[i]) = a0;
+            *reinterpret_cast<floatx4*>(kr + DHP / 2 + e[i]) = a1;
+            float* vt = lds.vt[buf];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                vt[(e[i] + u) * PV + key[i]] = v0[i][u];
+                vt[(half + e[i] + u) * PV + key[i]] = v1[i][u];
+            }
+        }
+    }
+};
+
+template <int DHP, int KB, bool ROPE, bool TS>
+__global__ __launch_bounds__(kThreads) void time_attention_f32(const TimeArgs a, int dh) {
+    static_assert(DHP % 16 == 0 && DHP <= 128, "head width");
+    static_assert(KB == 32 || KB == 64, "key block");
+    constexpr int kHalfP = DHP / 2;
+    constexpr int kSteps = kHalfP;  // K=2 per MFMA step: one dim from each lane half
+    constexpr int kTiles = F32Lds<DHP, KB, TS>::kTiles;
+    constexpr int kSub = KB / 32;  // 32-key S^T tiles per block
+    constexpr int PK = F32Lds<DHP, KB, TS>::kPitchK, PV = F32Lds<DHP, KB, TS>::kPitchV;
+    constexpr uint64_t kFull = KB == 64 ? ~0ull : 0xffffffffull;
+    __shared__ F32Lds<DHP, KB, TS> lds;
+
+    const float* __restrict__ qkv = static_cast<const float*>(a.qkv);
+    const int n = a.n, inner = a.inner, half = dh / 2;
+    const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+    const int j = lane % 32, g = lane / 32;
+    const uint32_t total = (uint32_t)a.rows * a.heads * a.qgroups;
+    const uint32_t logical = xcd_remap(blockIdx.x, total);
+    const int qg = logical % a.qgroups;
+    const int bh = logical / a.qgroups;
+    const int h = bh % a.heads, r = bh / a.heads;
+    TimeMask<TS> mask;
+    mask.init(a, r);
+    const int32_t* vrow = a.valid + (size_t)r * (TS ? a.enc : n);
+
+    // The wave's queries are requested first, so their latency overlaps the validity scan.
+    // Lane (j, g) holds dims g*dh/2 + s (s < dh/2) of query q0+j; the rest of its DHP/2 are zero.
+    const int q0 = (qg * kWaves + wave) * kQ;
+    const int nq = min(max(n - q0, 0), kQ);
+    floatx4 qa[kSteps / 4], qb[kSteps / 4], qc[kSteps / 4], qs[kSteps / 4];
+    if (j < nq) {
+        const int q = q0 + j;
+        const float* qp = qkv + ((size_t)r * n + q) * 3 * inner + h * dh;
+        int trow = q;
+        if (TS && ROPE && a.pos) trow = min(max(a.pos[(size_t)r * n + q], 0), a.table_rows - 1);
+#pragma unroll
+        for (int s4 = 0; s4 < kSteps / 4; s4++) {
+            if (4 * s4 < half) {
+                qa[s4] = *reinterpret_cast<const floatx4*>(qp + 4 * s4);
+                qb[s4] = *reinterpret_cast<const floatx4*>(qp + half + 4 * s4);
+                if (ROPE) {
+                    qc[s4] = *reinterpret_cast<const floatx4*>(a.table + (size_t)trow * dh + 4 * s4);
+                    qs[s4] = *reinterpret_cast<const floatx4*>(a.table + (size_t)trow * dh + half + 4 * s4);
+                }
+            }
+        }
+    }
+
+    // zero the padding of the K and V^T tiles once (staging never writes it)
+    if (dh < DHP) {
+        for (int i = tid; i < 2 * KB; i += kThreads) {
+            float* kr = &lds.k[i / KB][(i % KB) * PK];
+            for (int c = half; c < kHalfP; c++) kr[c] = kr[kHalfP + c] = 0.f;
+        }
+    }
+    if (dh < kTiles * 32) {
+        for (int i = tid; i < 2 * (kTiles * 32 - dh) * PV; i += kThreads) {
+            const int b = i / ((kTiles * 32 - dh) * PV), rest = i % ((kTiles * 32 - dh) * PV);
+            lds.vt[b][dh * PV + rest] = 0.f;
+        }
+    }
+    // key validity of every 64-key word of the row, and (Timestral) every token's table row
+    const int nwords = (n + kMaskBlock - 1) / kMaskBlock;
+    for (int w = wave; w < nwords; w += kWaves) {
+        const uint64_t bits = __ballot(mask.key_valid(vrow, w * kMaskBlock + lane));
+        if (lane == 0) lds.mask[w] = bits;
+    }
+    if (TS) {
+        for (int t = tid; t < n; t += kThreads)
+            lds.pos[t] = a.pos ? min(max(a.pos[(size_t)r * n + t], 0), a.table_rows - 1) : t;
+    }
+    __syncthreads();
+    // 64-key words any query of the workgroup can see (the same in every wave)
+    const int qlo = qg * kWaves * kQ, qhi = min(qlo + kWaves * kQ, n) - 1;
+    const uint64_t need = __ballot(lane < nwords && mask.any_allowed(lds.mask[lane], lane * kMaskBlock, qlo, qhi));
+    const int nblk = (n + KB - 1) / KB;
+    auto next_block = [&](int after) {
+        const int b = after + 1;
+        const int w = b * KB / kMaskBlock;
+        const uint64_t rest = (b >= nblk || w >= 64) ? 0ull : need & (~0ull << w);
+        if (!rest) return nblk;
+        const int wn = (int)__builtin_ctzll(rest);
+        return wn == w ? b : wn * kMaskBlock / KB;
+    };
+
+    // Q operands: rotated, scaled by qscale (log2(e) times the score scale)
+    float qreg[kSteps];
+#pragma unroll
+    for (int s4 = 0; s4 < kSteps / 4; s4++) {
+        floatx4 o = floatx4{0.f, 0.f, 0.f, 0.f};
+        if (j < nq && 4 * s4 < half) {
+            o = g == 0 ? qa[s4] : qb[s4];
+            if (ROPE) o = g == 0 ? qa[s4] * qc[s4] - qb[s4] * qs[s4] : qb[s4] * qc[s4] + qa[s4] * qs[s4];
+            o *= a.qscale;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) qreg[4 * s4 + u] = o[u];
+    }
+
+    const size_t row0 = (size_t)r * n;
+    const uint32_t stride_b = 3u * inner * 4u;
+    auto rk_at = [&](int b) {
+        const int k = b * KB;
+        const float* p = qkv + (row0 + k) * 3 * inner + inner + h * dh;
+        const uint32_t bytes = (uint32_t)(n - k) * stride_b - (uint32_t)(inner + h * dh) * 4u;
+        return make_rsrc(p, bytes);
+    };
+    auto rt_at = [&](int b) {
+        if (TS) return make_rsrc(a.table, (uint32_t)a.table_rows * dh * 4u);
+        const int k = b * KB;
+        return make_rsrc(a.table + (size_t)k * dh, (uint32_t)((n - k) * dh * 4));
+    };
+
+    int kb = next_block(-1);
+    KvStage<DHP, KB, ROPE, TS> stage;
+    stage.init(tid, inner, dh);
+    if (kb < nblk) {
+        stage.load(rk_at(kb), ROPE ? rt_at(kb) : rk_at(kb), lds.pos, kb * KB, n, tid, inner, dh);
+        stage.store(lds, 0, tid);
+    }
+    __syncthreads();
+
+    floatx16 o_acc[kTiles];
+#pragma unroll
+    for (int t = 0; t < kTiles; t++) o_acc[t] = floatx16{0};
+    float m_run = -INFINITY, l_run = 0.f;
+    int buf = 0;
+    // Settle every prologue load here: the compiler cannot prove that the divergent Q loads were
+    // consumed on all paths and would otherwise wait on them (vmcnt(0)) inside every iteration.
+    __builtin_amdgcn_s_waitcnt(0);
+
+    while (kb < nblk) {
+        const int next = next_block(kb);
+        if (next < nblk) stage.load(rk_at(next), ROPE ? rt_at(next) : rk_at(next), lds.pos, next * KB, n, tid, inner, dh);
+        // keep the prefetch above the block's MFMAs (the scheduler would sink it to its use)
+        __builtin_amdgcn_sched_barrier(0);
+
+        // the keys of this block the lane's query may see (bit i = key kb*KB + i)
+        const int k0 = kb * KB;
+        const uint64_t word = lds.mask[k0 / kMaskBlock];
+        const uint64_t allowed =
+            (mask.allowed(word, k0 & ~(kMaskBlock - 1), q0 + j) >> (k0 % kMaskBlock)) & kFull;
+        if (nq > 0 && __any(j < nq && allowed != 0)) {
+            // S^T = K Q^T over this block, one 32x32 tile per 32 keys
+            floatx16 s_acc[kSub];
+#pragma unroll
+            for (int sb = 0; sb < kSub; sb++) {
+                s_acc[sb] = floatx16{0};
+                const float* kp = &lds.k[buf][(32 * sb + j) * PK + g * kHalfP];
+#pragma unroll
+                for (int s4 = 0; s4 < kSteps / 4; s4++) {
+                    if (4 * s4 < half) {
+                        floatx4 kv = *reinterpret_cast<const floatx4*>(kp + 4 * s4);
+#pragma unroll
+                        for (int u = 0; u < 4; u++)
+                            s_acc[sb] =
+                                __builtin_amdgcn_mfma_f32_32x32x2f32(kv[u], qreg[4 * s4 + u], s_acc[sb], 0, 0, 0);
+                    }
+                }
+            }
+            // mask: reg rho of tile sb in lane (j, g) holds key 32sb + 8*(rho/4) + 4g + rho%4 of the block
+            if (__any(j < nq && allowed != kFull)) {
+#pragma unroll
+                for (int sb = 0; sb < kSub; sb++) {
+#pragma unroll
+                    for (int rho = 0; rho < 16; rho++) {
+                        int bit = 32 * sb + 8 * (rho / 4) + 4 * g + (rho % 4);
+                        if (!((allowed >> bit) & 1ull)) s_acc[sb][rho] = -INFINITY;
+                    }
+                }
+            }
+            float mx = s_acc[0][0];
+#pragma unroll
+            for (int sb = 0; sb < kSub; sb++)
+#pragma unroll
+                for (int rho = 0; rho < 16; rho++) mx = fmaxf(mx, s_acc[sb][rho]);
+            mx = pair_max(mx);
+            float m_new = fmaxf(m_run, mx);
+            float m_use = m_new == -INFINITY ? 0.f : m_new;
+            float alpha = fast_exp2(m_run - m_use);
+            m_run = m_new;
+            float rs = 0.f;
+#pragma unroll
+            for (int sb = 0; sb < kSub; sb++)
+#pragma unroll
+                for (int rho = 0; rho < 16; rho++) {
+                    s_acc[sb][rho] = fast_exp2(s_acc[sb][rho] - m_use);
+                    rs += s_acc[sb][rho];
+                }
+            l_run = l_run * alpha + rs;
+            // rescale O only when some query's running max moved (wave-uniform branch)
+            if (__any(alpha != 1.f)) {
+#pragma unroll
+                for (int t = 0; t < kTiles; t++) o_acc[t] *= alpha;
+            }
+            // O^T += V^T P^T: step c = 4a + u of tile sb uses keys 32sb + 8a + 4kk + u, P from s_acc[sb][c]
+#pragma unroll
+            for (int t = 0; t < kTiles; t++) {
+                if (32 * t < dh) {
+                    const float* vp = &lds.vt[buf][(32 * t + j) * PV + 4 * g];
+#pragma unroll
+                    for (int sb = 0; sb < kSub; sb++) {
+#pragma unroll
+                        for (int a4 = 0; a4 < 4; a4++) {
+                            floatx4 vv = *reinterpret_cast<const floatx4*>(vp + 32 * sb + 8 * a4);
+#pragma unroll
+                            for (int u = 0; u < 4; u++)
+                                o_acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv[u], s_acc[sb][4 * a4 + u], o_acc[t],
+                                                                                0, 0, 0);
+                        }
+                    }
+                }
+            }
+        }
+        if (next < nblk) stage.store(lds, buf ^ 1, tid);
+        __syncthreads();
+        buf ^= 1;
+        kb = next;
+    }
+
+    // every lane reaches the swap (its partner holds the other half of the same query)
+    const float l = pair_sum(l_run);
+    if (j < nq) {
+        const float inv = l > 0.f ? 1.f / l : 0.f;
+        const size_t tok = (size_t)r * n + q0 + j;
+        float* op = static_cast<float*>(a.out) + tok * inner + h * dh;
+        const float* gp = a.gate ? static_cast<const float*>(a.gate) + tok * inner + h * dh : nullptr;
+        // O^T reg 4a+u of lane (j, g) is dim 32t + 8a + 4g + u of query j
+#pragma unroll
+        for (int t = 0; t < kTiles; t++) {
+#pragma unroll
+            for (int a4 = 0; a4 < 4; a4++) {
+                const int e = 32 * t + 8 * a4 + 4 * g;
+                if (e < dh) {
+                    floatx4 v;
+#pragma unroll
+                    for (int u = 0; u < 4; u++) v[u] = o_acc[t][4 * a4 + u] * inv;
+                    if (gp) {
+                        // the output gate: att * sigmoid(g) (CpuTimestral.java:156-161)
+                        const floatx4 gv = *reinterpret_cast<const floatx4*>(gp + e);
+#pragma unroll
+                        for (int u = 0; u < 4; u++) v[u] *= 1.f / (1.f + fast_exp2(-gv[u] * kLog2e));
+                    }
+                    *reinterpret_cast<floatx4*>(op + e) = v;
+                }
+            }
+        }
+    }
+}
+
+}  // namespace
+
+template <int DHP, int KB, bool TS>
+static hipError_t launch_f32(TimeArgs a, int dh, hipStream_t stream) {
+    const int tiles = (a.n + kQ - 1) / kQ;
+    a.qgroups = (tiles + kWaves - 1) / kWaves;
+    const uint64_t grid = (uint64_t)a.rows * a.heads * a.qgroups;
+    if (a.table) {
+        hipLaunchKernelGGL((time_attention_f32<DHP, KB, true, TS>), dim3((uint32_t)grid), dim3(kThreads), 0, stream, a,
+                           dh);
+    } else {
+        hipLaunchKernelGGL((time_attention_f32<DHP, KB, false, TS>), dim3((uint32_t)grid), dim3(kThreads), 0, stream,
+                           a, dh);
+    }
+    return hipGetLastError();
+}
+
+// Key-block size: 32 by default; JITCAST_TIME_KB=64 selects 64-key blocks (read once).
+static int key_block() {
+    static int kb = [] {
+        const char* e = getenv("JITCAST_TIME_KB");
+        return (e && atoi(e) == 64) ? 64 : 32;
+    }();
+    return kb;
+}
+
+template <int KB, bool TS>
+static hipError_t dispatch_f32(const TimeArgs& a, int dh, hipStream_t stream) {
+    if (dh <= 16) return launch_f32<16, KB, TS>(a, dh, stream);
+    if (dh <= 32) return launch_f32<32, KB, TS>(a, dh, stream);
+    if (dh <= 64 || !TS) return launch_f32<64, KB, TS>(a, dh, stream);
+    if constexpr (TS) return launch_f32<128, KB, TS>(a, dh, stream);  // Chronos-2 heads are at most 64 wide
+    return hipErrorInvalidValue;
+}
+
+hipError_t time_attention_f32_launch(const TimeArgs& a, int dh, bool ts, hipStream_t stream) {
+    if (dh < 8 || dh > 128 || dh % 8) return hipErrorInvalidValue;
+    if (key_block() == 64)
+        return ts ? dispatch_f32<64, true>(a, dh, stream) : dispatch_f32<64, false>(a, dh, stream);
+    return ts ? dispatch_f32<32, true>(a, dh, stream) : dispatch_f32<32, false>(a, dh, stream);
+}
+
+int time_attention_max_tokens() { return kMaxTokens; }
+
+}  // namespace jc

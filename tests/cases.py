@@ -36,3 +36,22 @@ def group_sizes(seed: int, rows: int, lo: int, hi: int) -> np.ndarray:
         ids[r:e] = g
         r, g = e, g + 1
     return ids
+
+
+def ts_layout(seed: int, rows: int, enc: int, ll: int, h: int, known_frac: float = 0.0, max_start: int | None = None):
+    """A Timestral block layout in the shape BlockLayout.of produces (BlockLayout.java:77-148):
+    each row starts observing at patch s_r (attend_missing_patches: every patch from s_r on is a
+    valid key), rows are known covariates with probability known_frac, positions count patches from
+    the row's first observed patch (decoder tokens continue from ll). Returns (key_valid [rows, enc],
+    known [rows], position [rows, enc + h]) int32; the table row of a token is position + enc."""
+    ms = enc // 2 if max_start is None else max_start
+    starts = rng.randint(rng.stream_seed(seed, 4), rows, 0, ms)
+    k = np.arange(enc)[None, :]
+    key_valid = (k >= starts[:, None]).astype(np.int32)
+    known = (rng.uniform(rng.stream_seed(seed, 5), rows) < known_frac).astype(np.int32)
+    n = enc + h
+    t = np.arange(n)[None, :]
+    raw = np.where(t < enc, t, ll + t - enc)
+    first = np.where(starts < enc, starts, 0)
+    position = (raw - first[:, None]).astype(np.int32)
+    return key_valid, known, position
