@@ -10,7 +10,7 @@
 //
 // Layout: qkv [rows*n, 3*inner] (q | k | v, heads-major per token), out [rows*n, inner]. One
 // workgroup = 4 waves = 128 consecutive queries of one (row, head); each wave owns 32 queries.
-// Keys stream through LDS in blocks of KB, double-buffered; blocks no query of the workgroup can
+// Keys stream through LDS in blocks of KB = 32, double-buffered; blocks no query of the workgroup can
 // see are skipped, and a block no query of a wave can see costs that wave nothing but the barrier.
 //
 // MFMA mapping (v_mfma_f32_32x32x2_f32, 64 flops/clk/SIMD):
@@ -26,8 +26,6 @@
 #include "jc_common.hpp"
 #include "jc_kernels.hpp"
 #include "time_mask.hpp"
-
-#include <cstdlib>
 
 namespace jc {
 namespace {
@@ -124,8 +122,10 @@ struct KvStage {
     }
 };
 
-template <int DHP, int KB, bool ROPE, bool TS>
-__global__ __launch_bounds__(kThreads) void time_attention_f32(const TimeArgs a, int dh) {
+// EXACT: the head is exactly DHP wide, so every head-width expression folds to a constant
+template <int DHP, int KB, bool ROPE, bool TS, bool EXACT>
+__global__ __launch_bounds__(kThreads) void time_attention_f32(const TimeArgs a, int dh_rt) {
+    const int dh = EXACT ? DHP : dh_rt;
     static_assert(DHP % 16 == 0 && DHP <= 128, "head width");
     static_assert(KB == 32 || KB == 64, "key block");
     constexpr int kHalfP = DHP / 2;
@@ -376,44 +376,39 @@ __global__ __launch_bounds__(kThreads) void time_attention_f32(const TimeArgs a,
 
 }  // namespace
 
-template <int DHP, int KB, bool TS>
+template <int DHP, bool TS, bool EXACT>
 static hipError_t launch_f32(TimeArgs a, int dh, hipStream_t stream) {
+    constexpr int KB = 32;  // 32-key blocks (64 measured slower on config 1)
     const int tiles = (a.n + kQ - 1) / kQ;
     a.qgroups = (tiles + kWaves - 1) / kWaves;
     const uint64_t grid = (uint64_t)a.rows * a.heads * a.qgroups;
     if (a.table) {
-        hipLaunchKernelGGL((time_attention_f32<DHP, KB, true, TS>), dim3((uint32_t)grid), dim3(kThreads), 0, stream, a,
-                           dh);
+        hipLaunchKernelGGL((time_attention_f32<DHP, KB, true, TS, EXACT>), dim3((uint32_t)grid), dim3(kThreads), 0,
+                           stream, a, dh);
     } else {
-        hipLaunchKernelGGL((time_attention_f32<DHP, KB, false, TS>), dim3((uint32_t)grid), dim3(kThreads), 0, stream,
-                           a, dh);
+        hipLaunchKernelGGL((time_attention_f32<DHP, KB, false, TS, EXACT>), dim3((uint32_t)grid), dim3(kThreads), 0,
+                           stream, a, dh);
     }
     return hipGetLastError();
 }
 
-// Key-block size: 32 by default; JITCAST_TIME_KB=64 selects 64-key blocks (read once).
-static int key_block() {
-    static int kb = [] {
-        const char* e = getenv("JITCAST_TIME_KB");
-        return (e && atoi(e) == 64) ? 64 : 32;
-    }();
-    return kb;
+template <int DHP, bool TS>
+static hipError_t launch_f32_width(const TimeArgs& a, int dh, hipStream_t stream) {
+    return dh == DHP ? launch_f32<DHP, TS, true>(a, dh, stream) : launch_f32<DHP, TS, false>(a, dh, stream);
 }
 
-template <int KB, bool TS>
+template <bool TS>
 static hipError_t dispatch_f32(const TimeArgs& a, int dh, hipStream_t stream) {
-    if (dh <= 16) return launch_f32<16, KB, TS>(a, dh, stream);
-    if (dh <= 32) return launch_f32<32, KB, TS>(a, dh, stream);
-    if (dh <= 64 || !TS) return launch_f32<64, KB, TS>(a, dh, stream);
-    if constexpr (TS) return launch_f32<128, KB, TS>(a, dh, stream);  // Chronos-2 heads are at most 64 wide
+    if (dh <= 16) return launch_f32_width<16, TS>(a, dh, stream);
+    if (dh <= 32) return launch_f32_width<32, TS>(a, dh, stream);
+    if (dh <= 64 || !TS) return launch_f32_width<64, TS>(a, dh, stream);
+    if constexpr (TS) return launch_f32_width<128, TS>(a, dh, stream);  // Chronos-2 heads are at most 64 wide
     return hipErrorInvalidValue;
 }
 
 hipError_t time_attention_f32_launch(const TimeArgs& a, int dh, bool ts, hipStream_t stream) {
     if (dh < 8 || dh > 128 || dh % 8) return hipErrorInvalidValue;
-    if (key_block() == 64)
-        return ts ? dispatch_f32<64, true>(a, dh, stream) : dispatch_f32<64, false>(a, dh, stream);
-    return ts ? dispatch_f32<32, true>(a, dh, stream) : dispatch_f32<32, false>(a, dh, stream);
+    return ts ? dispatch_f32<true>(a, dh, stream) : dispatch_f32<false>(a, dh, stream);
 }
 
 int time_attention_max_tokens() { return kMaxTokens; }

@@ -265,9 +265,11 @@ __device__ __forceinline__ float from_bits(uint32_t b) {
 constexpr float kSumHi = 65536.f;
 constexpr float kSumLo = 1.0f / 65536.f;
 
-template <typename T, int DHP, int NW, bool ROPE, bool TS>
+// EXACT: the head is exactly DHP wide, so every head-width expression folds to a constant
+template <typename T, int DHP, int NW, bool ROPE, bool TS, bool EXACT>
 __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(NW >= 4 && DHP <= 64 && !TS ? 3 : 2)))
-void time_attention_lp(const TimeArgs a, int dh) {
+void time_attention_lp(const TimeArgs a, int dh_rt) {
+    const int dh = EXACT ? DHP : dh_rt;
     static_assert(DHP % 16 == 0 && DHP <= 128, "head width");
     constexpr int NT = NW * kWave;
     constexpr int kHalfP = DHP / 2;
@@ -596,16 +598,16 @@ void time_attention_lp(const TimeArgs a, int dh) {
     }
 }
 
-template <typename T, int DHP, int NW, bool TS>
+template <typename T, int DHP, int NW, bool TS, bool EXACT>
 hipError_t launch_lp_nw(TimeArgs a, int dh, hipStream_t stream) {
     const int tiles = (a.n + kQ - 1) / kQ;
     a.qgroups = (tiles + NW - 1) / NW;
     const uint64_t grid = (uint64_t)a.rows * a.heads * a.qgroups;
     if (a.table) {
-        hipLaunchKernelGGL((time_attention_lp<T, DHP, NW, true, TS>), dim3((uint32_t)grid), dim3(NW * kWave), 0,
+        hipLaunchKernelGGL((time_attention_lp<T, DHP, NW, true, TS, EXACT>), dim3((uint32_t)grid), dim3(NW * kWave), 0,
                            stream, a, dh);
     } else {
-        hipLaunchKernelGGL((time_attention_lp<T, DHP, NW, false, TS>), dim3((uint32_t)grid), dim3(NW * kWave), 0,
+        hipLaunchKernelGGL((time_attention_lp<T, DHP, NW, false, TS, EXACT>), dim3((uint32_t)grid), dim3(NW * kWave), 0,
                            stream, a, dh);
     }
     return hipGetLastError();
@@ -615,18 +617,23 @@ hipError_t launch_lp_nw(TimeArgs a, int dh, hipStream_t stream) {
 // (n = 513, 17 tiles): 4 waves 0.511 ms, 6 waves 0.634 ms, 8 waves 0.611 ms. The kernel is bound by
 // the latency of each workgroup's prologue and per-block loads; three 4-wave workgroups per CU
 // overlap those better than two 6-wave ones, which outweighs the extra idle query slots.
-template <typename T, int DHP, bool TS>
+template <typename T, int DHP, bool TS, bool EXACT>
 hipError_t launch_lp(const TimeArgs& a, int dh, hipStream_t stream) {
-    if ((a.n + kQ - 1) / kQ <= 2) return launch_lp_nw<T, DHP, 2, TS>(a, dh, stream);
-    return launch_lp_nw<T, DHP, 4, TS>(a, dh, stream);
+    if ((a.n + kQ - 1) / kQ <= 2) return launch_lp_nw<T, DHP, 2, TS, EXACT>(a, dh, stream);
+    return launch_lp_nw<T, DHP, 4, TS, EXACT>(a, dh, stream);
+}
+
+template <typename T, int DHP, bool TS>
+hipError_t launch_lp_width(const TimeArgs& a, int dh, hipStream_t stream) {
+    return dh == DHP ? launch_lp<T, DHP, TS, true>(a, dh, stream) : launch_lp<T, DHP, TS, false>(a, dh, stream);
 }
 
 template <typename T, bool TS>
 hipError_t dispatch_lp(const TimeArgs& a, int dh, hipStream_t stream) {
-    if (dh <= 16) return launch_lp<T, 16, TS>(a, dh, stream);
-    if (dh <= 32) return launch_lp<T, 32, TS>(a, dh, stream);
-    if (dh <= 64 || !TS) return launch_lp<T, 64, TS>(a, dh, stream);
-    if constexpr (TS) return launch_lp<T, 128, TS>(a, dh, stream);  // Chronos-2 heads are at most 64 wide
+    if (dh <= 16) return launch_lp_width<T, 16, TS>(a, dh, stream);
+    if (dh <= 32) return launch_lp_width<T, 32, TS>(a, dh, stream);
+    if (dh <= 64 || !TS) return launch_lp_width<T, 64, TS>(a, dh, stream);
+    if constexpr (TS) return launch_lp_width<T, 128, TS>(a, dh, stream);  // Chronos-2 heads are at most 64 wide
     return hipErrorInvalidValue;
 }
 
