@@ -121,7 +121,8 @@ int jc_c2_time_attention(jc_ctx *ctx, const void *qkv, void *out, const int32_t 
  * dh, inner) (J/chronos2/tornado/Chronos2Kernels.java:473-474), oracle CpuChronos2.java:230-282.
  *   qkv, out     device, as jc_c2_time_attention (the group sublayer's own projection)
  *   group_start  device int32 [rows]; group_end device int32 [rows] (jc_c2_group_bounds)
- *   dh           a multiple of 16, at most 64
+ *   dh           a multiple of 8, at most 64 (the reference takes multiples of 16); fp32 only
+ *                (bf16/fp16 return JC_EUNSUPPORTED)
  */
 int jc_c2_group_attention(jc_ctx *ctx, const void *qkv, void *out, const int32_t *live, const int32_t *group_start,
                           const int32_t *group_end, int rows, int n, int heads, int dh, int inner, int dtype);
@@ -167,6 +168,27 @@ int jc_ts_time_attention(jc_ctx *ctx, const void *qkv, void *out, const int32_t 
  * (J/timestral/tornado/TimestralKernels.java:572-578); the attention entry points fuse it.
  */
 int jc_ts_gate(jc_ctx *ctx, void *att, const void *g, int64_t count, int dtype);
+
+/* ---- Timestral variate attention -------------------------------------------------------------- */
+
+/*
+ * Attention across the rows of each series at every token slot, per head, with scores scaled by
+ * 1/sqrt(dh) under BlockLayout.variateAllowed: row q reads row k of its group [group_start[q],
+ * group_end[q]) when k == q, or when (at an encoder slot t < enc) key_valid[k][t] and, with
+ * covariates, not (role[q] != TARGET and role[k] == TARGET) and not (role[q] == KNOWN and role[k] !=
+ * KNOWN); out *= sigmoid(gate) when gate is not NULL. Groups are contiguous runs of rows.
+ * Replaces TimestralKernels.variateAttention(qkv, out, keyValid, groupStart, groupEnd, role,
+ * covariates, rows, enc, n, heads, dh, d) and TimestralKernels.gate
+ * (J/timestral/tornado/TimestralKernels.java:290-292, 573); oracle CpuTimestral.java:261-314;
+ * masks BlockLayout.java:223-243.
+ *   key_valid  device int32 [rows*enc]; role device int32 [rows] (0 TARGET, 1 PAST, 2 KNOWN;
+ *              BlockInput.java:35-37), may be NULL when covariates == 0
+ *   gate       device fp32 [rows*n, d] or NULL; dtype: JC_F32 (bf16/fp16 return JC_EUNSUPPORTED)
+ *   dh         a multiple of 8, at most 128; d >= heads*dh
+ */
+int jc_ts_variate_attention(jc_ctx *ctx, const void *qkv, void *out, const int32_t *key_valid,
+                            const int32_t *group_start, const int32_t *group_end, const int32_t *role, int covariates,
+                            const void *gate, int rows, int enc, int n, int heads, int dh, int d, int dtype);
 
 /* ---- host-side layout (the per-call work the reference does in Java before each upload) ------- */
 

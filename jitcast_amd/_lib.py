@@ -61,6 +61,7 @@ SIGNATURES = {
     "jc_ts_rope_table": (_i, [_i, _i, _i, _i, _f, _vp]),
     "jc_ts_time_attention": (_i, [_vp, _vp, _vp, _i32p, _i32p, _i32p, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i]),
     "jc_ts_gate": (_i, [_vp, _vp, _vp, _c.c_int64, _i]),
+    "jc_ts_variate_attention": (_i, [_vp, _vp, _vp, _i32p, _i32p, _i32p, _i32p, _i, _vp, _i, _i, _i, _i, _i, _i, _i]),
     "jc_c2_live": (_i, [_vp, _i, _i, _i, _i, _i, _vp]),
     "jc_c2_group_order": (_i, [_vp, _i, _vp, _c.POINTER(_i)]),
     "jc_c2_group_bounds": (_i, [_vp, _i, _vp, _vp]),

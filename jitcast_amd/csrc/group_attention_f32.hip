@@ -1,0 +1,293 @@
+// Group (cross-series) attention for gfx950, FP32 path: Chronos-2's group attention and
+// Timestral's variate attention.
+//
+// Chronos-2 replaces Chronos2Kernels.groupAttention(qkv, out, live, groupStart, groupEnd, rows, n,
+// heads, dh, inner) (Chronos2Kernels.java:466-682; oracle CpuChronos2.java:230-282): at every token
+// slot t, row i attends the rows j of its group (groupStart[i] <= j < groupEnd[i], groups are
+// contiguous runs of rows) whose token at t is live; unscaled scores, no positional encoding; zeros
+// when no key is live.
+// Timestral replaces TimestralKernels.variateAttention(qkv, out, keyValid, groupStart, groupEnd,
+// role, covariates, rows, enc, n, heads, dh, d) and the gate (TimestralKernels.java:280-446,
+// 572-578; oracle CpuTimestral.java:156-161, 261-314): scores scaled by 1/sqrt(dh) under
+// BlockLayout.variateAllowed (BlockLayout.java:223-243): an encoder slot only where the key row's
+// patch is a valid key; with covariates a covariate row never reads a target row and a known row
+// reads only known rows; a row always reads itself. The optional sigmoid gate is fused.
+//
+// The stage reads q|k|v once and writes out once, about 10 flop per byte: it is HBM-bound, so the
+// kernel is built around the memory stream. One wave per (16-row tile, slot) owns the groups that
+// START in its tile (found by a ballot on groupStart[i] == i), so each row's q, k and v are fetched
+// from HBM once; everything lives in registers (no LDS, no barriers). The wave's work is a flat
+// stream of jobs (group, chunk of up to 4 query tiles (2 for heads over 64 wide), head, 16-key
+// tile): the chunk's queries and output accumulators stay in registers while the group's key tiles
+// stream past, each K/V tile used by every query tile right after it lands, and the next job's K/V loads are issued before this
+// job's MFMAs (register double-buffering). The online softmax across key tiles makes any group size
+// work; a group past 64 rows re-streams its keys once per further 64-row chunk.
+//
+// Operand layouts (16x16x4 f32: A lane i+16kk = A[i][kk], B lane j+16kk = B[kk][j],
+// D lane j+16g reg r = D[4g+r][j]):
+//   S^T[key][q] = K Q^T: step s = 4m+u contracts dim 16m + 4kk + u, so each lane's K and Q come
+//                        from one 16-byte load per m and a 64-byte run per row per load.
+//   O^T[e][q] += V^T P^T: step c contracts key 4kk + c, whose P^T is S^T's reg c; V^T is loaded
+//                        per lane as V[key][e] (16 rows x 64 contiguous bytes per load).
+#include "jc_common.hpp"
+#include "jc_kernels.hpp"
+
+namespace jc {
+namespace {
+
+constexpr int kRT = 16;  // rows per tile (queries and keys)
+
+// max / sum over the four lanes j, j+16, j+32, j+48 (v_permlane16_swap then v_permlane32_swap)
+__device__ __forceinline__ float quad_max(float v) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    return pair_max(v);
+}
+
+__device__ __forceinline__ float quad_sum(float v) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    return pair_sum(v);
+}
+
+// A position in the wave's job stream: group [gs, ge), query chunk qc (up to kQT tiles of 16
+// rows), head h, key tile kt.
+struct Job {
+    int gs, ge, qc, h, kt;
+    uint32_t rest;  // starts of the tile's remaining groups (bit b = row r0 + b)
+    bool valid;
+};
+
+
+template <int DHP, bool TS, bool EXACT>
+__global__ __launch_bounds__(kWave) void group_attention_f32(const GroupArgs a, int dh_rt) {
+    static_assert(DHP % 16 == 0 && DHP <= 128, "head width");
+    constexpr int kM = DHP / 16;            // 16-dim groups: K/Q loads per lane, and output dim tiles
+    constexpr int kQT = DHP <= 64 ? 4 : 2;  // query tiles held in registers at once
+    const int dh = EXACT ? DHP : dh_rt;
+    const float* __restrict__ qkv = a.qkv;
+    const int rows = a.rows, n = a.n, heads = a.heads, inner = a.inner;
+    const int lane = threadIdx.x;
+    const int j = lane % 16, g = lane / 16;
+    const uint32_t total = (uint32_t)a.rtiles * n;
+    const uint32_t logical = xcd_remap(blockIdx.x, total);
+    const int t = logical / a.rtiles, rt = logical % a.rtiles;
+    const int r0 = rt * kRT;
+    const int nr = min(kRT, rows - r0);
+    const size_t stride = 3 * (size_t)inner;  // floats per token of qkv
+    const size_t tok_n = (size_t)n;
+    const bool enc_slot = TS && t < a.enc;
+    const bool cov = TS && a.covariates != 0 && a.role != nullptr;
+
+    // the groups starting in this tile
+    const uint32_t starts = (uint32_t)__ballot(lane < nr && a.gstart[r0 + lane] == r0 + lane) & 0xffffu;
+    if (starts == 0) return;
+
+    auto first_of = [&](uint32_t rest) {
+        Job jb;
+        jb.valid = rest != 0;
+        int b = jb.valid ? __builtin_ctz(rest) : 0;
+        jb.gs = r0 + b;
+        // clamped into [gs+1, rows]: a group always holds its first row and only rows that exist
+        jb.ge = jb.valid ? min(max(a.gend[jb.gs], jb.gs + 1), rows) : jb.gs + 1;
+        jb.qc = 0;
+        jb.h = 0;
+        jb.kt = 0;
+        jb.rest = jb.valid ? rest & (rest - 1) : 0;
+        return jb;
+    };
+    // key tiles innermost, so a K/V tile is used by every resident query tile right after it lands
+    auto advance = [&](Job jb) {
+        const int tiles = (jb.ge - jb.gs + kRT - 1) / kRT;
+        if (++jb.kt < tiles) return jb;
+        jb.kt = 0;
+        if (++jb.h < heads) return jb;
+        jb.h = 0;
+        if (++jb.qc * kQT < tiles) return jb;
+        return first_of(jb.rest);
+    };
+    // K (A operand) and V^T (A operand of PV) of a job's key tile; rows past the group are clamped
+    // (finite, masked). In lanes j < 16: the validity of key 16kt + j and (Timestral) its role.
+    struct Kv {
+        floatx4 k[kM];
+        float v[kM][4];
+        int valid, role;
+    };
+    auto load_kv = [&](const Job& jb, Kv& d) {
+        const int kbase = jb.gs + kRT * jb.kt;
+        const int krow = min(kbase + j, jb.ge - 1);
+        const float* kp = qkv + ((size_t)krow * tok_n + t) * stride + inner + jb.h * dh + 4 * g;
+        const bool in_group = g == 0 && kbase + j < jb.ge;
+        if (TS) {
+            d.valid = in_group && (!enc_slot || a.valid[(size_t)krow * a.enc + t] != 0);
+            d.role = cov ? a.role[krow] : 0;
+        } else {
+            d.valid = in_group ? a.valid[(size_t)krow * tok_n + t] : 0;
+            d.role = 0;
+        }
+#pragma unroll
+        for (int m = 0; m < kM; m++)
+            d.k[m] = (EXACT || 16 * m + 4 * g < dh) ? *reinterpret_cast<const floatx4*>(kp + 16 * m)
+                                                     : floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const int vrow = min(kbase + 4 * g + c, jb.ge - 1);
+            const float* vp = qkv + ((size_t)vrow * tok_n + t) * stride + 2 * inner + jb.h * dh + j;
+#pragma unroll
+            for (int m = 0; m < kM; m++) d.v[m][c] = (EXACT || 16 * m + j < dh) ? vp[16 * m] : 0.f;
+        }
+    };
+
+    Job cur = first_of(starts);
+    Kv dc, dn;
+    load_kv(cur, dc);
+
+    float qreg[kQT][4 * kM];  // resident query tiles (B operand), scaled by qscale
+    floatx4 o_acc[kQT][kM];
+    float m_run[kQT], l_run[kQT];
+    int q_role[kQT];
+    while (cur.valid) {
+        const int tiles = (cur.ge - cur.gs + kRT - 1) / kRT;
+        const int nq = min(kQT, tiles - kQT * cur.qc);  // query tiles in this chunk
+        if (cur.kt == 0) {
+            // a new (group, chunk, head): load its query tiles and reset the softmax state
+#pragma unroll
+            for (int qi = 0; qi < kQT; qi++) {
+                if (qi < nq) {
+                    const int qrow = min(cur.gs + kRT * (kQT * cur.qc + qi) + j, cur.ge - 1);
+                    const float* qp = qkv + ((size_t)qrow * tok_n + t) * stride + cur.h * dh + 4 * g;
+#pragma unroll
+                    for (int m = 0; m < kM; m++) {
+                        floatx4 x = (EXACT || 16 * m + 4 * g < dh) ? *reinterpret_cast<const floatx4*>(qp + 16 * m)
+                                                                    : floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                        for (int u = 0; u < 4; u++) qreg[qi][4 * m + u] = x[u] * a.qscale;
+                    }
+                    q_role[qi] = cov ? a.role[qrow] : 0;
+                }
+#pragma unroll
+                for (int m = 0; m < kM; m++) o_acc[qi][m] = floatx4{0.f, 0.f, 0.f, 0.f};
+                m_run[qi] = -INFINITY;
+                l_run[qi] = 0.f;
+            }
+        }
+        const Job nxt = advance(cur);
+        load_kv(nxt, dn);  // in flight under this job's MFMAs (an invalid job reloads in-bounds rows)
+        __builtin_amdgcn_sched_barrier(0);
+
+        // bit b: key gs + 16kt + b is valid (and, for Timestral, a target / known-covariate row)
+        const uint32_t vbits = (uint32_t)__ballot(dc.valid != 0) & 0xffffu;
+        const uint32_t tbits = cov ? (uint32_t)__ballot(g == 0 && dc.role == 0) & 0xffffu : 0u;
+        const uint32_t kbits = cov ? (uint32_t)__ballot(g == 0 && dc.role == 2) & 0xffffu : 0u;
+        const int kbase = cur.gs + kRT * cur.kt;
+#pragma unroll
+        for (int qi = 0; qi < kQT; qi++) {
+            if (qi < nq) {
+                // the keys query row qrow may read (BlockLayout.variateAllowed for Timestral)
+                uint32_t allowed = vbits;
+                if (TS) {
+                    const int qrow = cur.gs + kRT * (kQT * cur.qc + qi) + j;
+                    uint32_t forbid = 0;
+                    if (cov) {
+                        if (q_role[qi] != 0) forbid |= tbits;             // covariate rows never read targets
+                        if (q_role[qi] == 2) forbid |= ~kbits & 0xffffu;  // known rows read known rows only
+                    }
+                    const int self = qrow - kbase;
+                    allowed = (vbits & ~forbid) | ((self >= 0 && self < kRT) ? (1u << self) : 0u);
+                }
+                floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int m = 0; m < kM; m++) {
+                    if (EXACT || 16 * m < dh) {
+#pragma unroll
+                        for (int u = 0; u < 4; u++)
+                            s = __builtin_amdgcn_mfma_f32_16x16x4f32(dc.k[m][u], qreg[qi][4 * m + u], s, 0, 0, 0);
+                    }
+                }
+                // reg r of lane (j, g) is key 16kt + 4g + r of the group (every row of the job is in it)
+#pragma unroll
+                for (int r = 0; r < 4; r++) s[r] = ((allowed >> (4 * g + r)) & 1u) ? s[r] : -INFINITY;
+                const float mx = quad_max(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])));
+                const float m_new = fmaxf(m_run[qi], mx);
+                const float m_use = m_new == -INFINITY ? 0.f : m_new;
+                const float alpha = fast_exp2(m_run[qi] - m_use);
+                m_run[qi] = m_new;
+#pragma unroll
+                for (int r = 0; r < 4; r++) s[r] = fast_exp2(s[r] - m_use);
+                l_run[qi] = l_run[qi] * alpha + (s[0] + s[1]) + (s[2] + s[3]);
+#pragma unroll
+                for (int m = 0; m < kM; m++) {
+                    if (EXACT || 16 * m < dh) {
+                        o_acc[qi][m] *= alpha;
+#pragma unroll
+                        for (int c = 0; c < 4; c++)
+                            o_acc[qi][m] =
+                                __builtin_amdgcn_mfma_f32_16x16x4f32(dc.v[m][c], s[c], o_acc[qi][m], 0, 0, 0);
+                    }
+                }
+            }
+        }
+
+        if (cur.kt == tiles - 1) {
+#pragma unroll
+            for (int qi = 0; qi < kQT; qi++) {
+                if (qi < nq) {
+                    const float l = quad_sum(l_run[qi]);
+                    const int qrow = cur.gs + kRT * (kQT * cur.qc + qi) + j;
+                    if (qrow < cur.ge) {
+                        const float inv = l > 0.f ? 1.f / l : 0.f;
+                        const size_t off = ((size_t)qrow * tok_n + t) * inner + cur.h * dh + 4 * g;
+                        // O^T reg r of lane (j, g) in dim tile m is dim 16m + 4g + r of the query
+#pragma unroll
+                        for (int m = 0; m < kM; m++) {
+                            if (EXACT || 16 * m + 4 * g < dh) {
+                                floatx4 v = o_acc[qi][m] * inv;
+                                if (a.gate) {
+                                    // the output gate: att * sigmoid(g) (CpuTimestral.java:156-161)
+                                    const floatx4 gv = *reinterpret_cast<const floatx4*>(a.gate + off + 16 * m);
+#pragma unroll
+                                    for (int u = 0; u < 4; u++) v[u] *= 1.f / (1.f + fast_exp2(-gv[u] * kLog2e));
+                                }
+                                *reinterpret_cast<floatx4*>(a.out + off + 16 * m) = v;
+                            }
+                        }
+                    }
+                }
+            }
+        }
+        cur = nxt;
+        dc = dn;
+    }
+}
+
+}  // namespace
+
+template <int DHP, bool TS, bool EXACT>
+static hipError_t launch_group(GroupArgs a, int dh, hipStream_t stream) {
+    a.rtiles = (a.rows + kRT - 1) / kRT;
+    const uint64_t grid = (uint64_t)a.rtiles * a.n;
+    hipLaunchKernelGGL((group_attention_f32<DHP, TS, EXACT>), dim3((uint32_t)grid), dim3(kWave), 0, stream, a, dh);
+    return hipGetLastError();
+}
+
+template <int DHP, bool TS>
+static hipError_t launch_group_width(const GroupArgs& a, int dh, hipStream_t stream) {
+    return dh == DHP ? launch_group<DHP, TS, true>(a, dh, stream) : launch_group<DHP, TS, false>(a, dh, stream);
+}
+
+template <bool TS>
+static hipError_t dispatch_group(const GroupArgs& a, int dh, hipStream_t stream) {
+    if (dh <= 16) return launch_group_width<16, TS>(a, dh, stream);
+    if (dh <= 32) return launch_group_width<32, TS>(a, dh, stream);
+    if (dh == 48) return launch_group<48, TS, true>(a, dh, stream);
+    if (dh <= 64 || !TS) return launch_group_width<64, TS>(a, dh, stream);
+    if constexpr (TS) return launch_group_width<128, TS>(a, dh, stream);  // Chronos-2 heads are at most 64 wide
+    return hipErrorInvalidValue;
+}
+
+hipError_t group_attention_f32_launch(const GroupArgs& a, int dh, bool ts, hipStream_t stream) {
+    if (dh < 8 || dh > 128 || dh % 8) return hipErrorInvalidValue;
+    return ts ? dispatch_group<true>(a, dh, stream) : dispatch_group<false>(a, dh, stream);
+}
+
+}  // namespace jc

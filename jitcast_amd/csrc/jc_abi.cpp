@@ -338,28 +338,74 @@ int jc_ts_gate(jc_ctx* ctx, void* att, const void* g, int64_t count, int dtype) 
     return e == hipSuccess ? JC_OK : hip_fail(W, e);
 }
 
+static int check_group_common(const char* W, const void* qkv, const void* out, const void* gate, const int32_t* gs,
+                              const int32_t* ge, int rows, int n, int heads, int dh, int inner, int dtype, int max_dh) {
+    if (rows < 0 || n < 0 || heads < 1) return fail(JC_EINVAL, "%s: bad shape rows=%d n=%d heads=%d", W, rows, n, heads);
+    if (dh < 8 || dh > max_dh || dh % 8)
+        return fail(JC_EINVAL, "%s: head width %d (need a multiple of 8, <= %d)", W, dh, max_dh);
+    if (inner < heads * dh || inner % 4)
+        return fail(JC_EINVAL, "%s: inner %d (need >= heads*dh = %d and a multiple of 4)", W, inner, heads * dh);
+    if (dtype != JC_F32 && dtype != JC_BF16 && dtype != JC_F16) return fail(JC_EINVAL, "%s: dtype %d", W, dtype);
+    if (dtype != JC_F32) return fail(JC_EUNSUPPORTED, "%s: dtype %d is not built yet (fp32 only)", W, dtype);
+    if ((size_t)rows * n == 0) return JC_OK;
+    if (!qkv || !out || !gs || !ge) return fail(JC_EINVAL, "%s: null device pointer", W);
+    if (!aligned16(qkv) || !aligned16(out) || (gate && !aligned16(gate)))
+        return fail(JC_EINVAL, "%s: qkv, out and gate must be 16-byte aligned", W);
+    if ((uint64_t)((rows + 15) / 16) * n > 0x7fffffffull) return fail(JC_EINVAL, "%s: grid too large", W);
+    return JC_OK;
+}
+
 int jc_c2_group_attention(jc_ctx* ctx, const void* qkv, void* out, const int32_t* live, const int32_t* group_start,
                           const int32_t* group_end, int rows, int n, int heads, int dh, int inner, int dtype) {
     const char* W = "jc_c2_group_attention";
     int rc = use(ctx, W);
     if (rc) return rc;
-    if (rows < 0 || n < 0 || heads < 1) return fail(JC_EINVAL, "%s: bad shape rows=%d n=%d heads=%d", W, rows, n, heads);
-    if (dh < 16 || dh > 64 || dh % 16)
-        return fail(JC_EINVAL, "%s: head width %d (need a multiple of 16, <= 64)", W, dh);
-    if (inner < heads * dh || inner % 4)
-        return fail(JC_EINVAL, "%s: inner %d (need >= heads*dh = %d and a multiple of 4)", W, inner, heads * dh);
-    if (dtype != JC_F32 && dtype != JC_BF16 && dtype != JC_F16) return fail(JC_EINVAL, "%s: dtype %d", W, dtype);
-    if ((size_t)rows * n == 0) return JC_OK;
-    if (!qkv || !out || !live || !group_start || !group_end) return fail(JC_EINVAL, "%s: null device pointer", W);
-    if (!aligned16(qkv) || !aligned16(out)) return fail(JC_EINVAL, "%s: qkv and out must be 16-byte aligned", W);
-    if ((uint64_t)((rows + 15) / 16) * n > 0x7fffffffull) return fail(JC_EINVAL, "%s: grid too large", W);
-    hipError_t e;
-    if (dtype == JC_F32) {
-        e = jc::c2_group_attention_f32_launch((const float*)qkv, (float*)out, live, group_start, group_end, rows, n,
-                                              heads, dh, inner, ctx->stream);
-    } else {
-        return fail(JC_EUNSUPPORTED, "%s: dtype %d is not built yet", W, dtype);
-    }
+    rc = check_group_common(W, qkv, out, nullptr, group_start, group_end, rows, n, heads, dh, inner, dtype, 64);
+    if (rc || (size_t)rows * n == 0) return rc;
+    if (!live) return fail(JC_EINVAL, "%s: null live mask", W);
+    jc::GroupArgs a{};
+    a.qkv = (const float*)qkv;
+    a.out = (float*)out;
+    a.valid = live;
+    a.gstart = group_start;
+    a.gend = group_end;
+    a.rows = rows;
+    a.n = n;
+    a.heads = heads;
+    a.inner = inner;
+    a.enc = n;
+    a.qscale = 1.4426950408889634f;  // unscaled scores, exp via exp2
+    hipError_t e = jc::group_attention_f32_launch(a, dh, false, ctx->stream);
+    return e == hipSuccess ? JC_OK : hip_fail(W, e);
+}
+
+int jc_ts_variate_attention(jc_ctx* ctx, const void* qkv, void* out, const int32_t* key_valid,
+                            const int32_t* group_start, const int32_t* group_end, const int32_t* role, int covariates,
+                            const void* gate, int rows, int enc, int n, int heads, int dh, int d, int dtype) {
+    const char* W = "jc_ts_variate_attention";
+    int rc = use(ctx, W);
+    if (rc) return rc;
+    if (enc < 0 || n < enc) return fail(JC_EINVAL, "%s: token counts (need 0 <= enc <= n; got enc=%d n=%d)", W, enc, n);
+    rc = check_group_common(W, qkv, out, gate, group_start, group_end, rows, n, heads, dh, d, dtype, 128);
+    if (rc || (size_t)rows * n == 0) return rc;
+    if (enc > 0 && !key_valid) return fail(JC_EINVAL, "%s: null key_valid", W);
+    if (covariates && !role) return fail(JC_EINVAL, "%s: covariates without a role array", W);
+    jc::GroupArgs a{};
+    a.qkv = (const float*)qkv;
+    a.out = (float*)out;
+    a.valid = key_valid;
+    a.gstart = group_start;
+    a.gend = group_end;
+    a.role = role;
+    a.gate = (const float*)gate;
+    a.rows = rows;
+    a.n = n;
+    a.heads = heads;
+    a.inner = d;
+    a.enc = enc;
+    a.covariates = covariates;
+    a.qscale = (float)(1.4426950408889634 / std::sqrt((double)dh));
+    hipError_t e = jc::group_attention_f32_launch(a, dh, true, ctx->stream);
     return e == hipSuccess ? JC_OK : hip_fail(W, e);
 }
 

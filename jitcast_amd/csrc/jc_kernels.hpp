@@ -16,9 +16,25 @@ hipError_t time_attention_lp_launch(const TimeArgs& a, int dh, bool ts, bool fp1
 int time_attention_max_tokens();
 // att[i] *= sigmoid(g[i]) for i < count (dtype: 0 fp32, 1 bf16, 2 fp16)
 hipError_t gate_launch(void* att, const void* g, uint64_t count, int dtype, hipStream_t stream);
-hipError_t c2_group_attention_f32_launch(const float* qkv, float* out, const int32_t* live, const int32_t* gs,
-                                         const int32_t* ge, int rows, int n, int heads, int dh, int inner,
-                                         hipStream_t stream);
+// The arguments of the group-attention kernels (by value).
+struct GroupArgs {
+    const float* qkv;       // [rows*n, 3*inner]
+    float* out;             // [rows*n, inner]
+    const int32_t* valid;   // Chronos-2: live [rows*n]; Timestral: keyValid [rows*enc]
+    const int32_t* gstart;  // [rows]
+    const int32_t* gend;    // [rows]
+    const int32_t* role;    // Timestral: [rows] TARGET 0 / PAST 1 / KNOWN 2, or null
+    const float* gate;      // [rows*n, inner]: out *= sigmoid(gate); or null
+    int rows, n, heads, inner;
+    int enc;                // Timestral's encoder slots (keyValid applies to t < enc)
+    int covariates;         // Timestral: whether the block runs the covariate rules
+    float qscale;           // score scale times log2(e), folded into q
+    int rtiles;             // 16-row tiles, set by the launcher
+};
+
+// Chronos-2 group attention (ts = false) or Timestral variate attention (ts = true); a.rtiles is
+// set by the launcher. dh a multiple of 8, at most 128 (64 for Chronos-2).
+hipError_t group_attention_f32_launch(const GroupArgs& a, int dh, bool ts, hipStream_t stream);
 
 hipError_t fill_normal_launch(float* out, uint64_t count, uint64_t stream_seed, double mean, double stdv,
                               hipStream_t stream);

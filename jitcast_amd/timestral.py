@@ -5,6 +5,7 @@ on the GPU, and launches on torch's current stream:
 
   time_attention   TimestralKernels.rope + timeAttention + gate
                    (J/timestral/tornado/TimestralKernels.java:77-78, 114-115, 573), fused
+  variate_attention  TimestralKernels.variateAttention + gate (TimestralKernels.java:290-292, 573)
   gate             TimestralKernels.gate (TimestralKernels.java:572-578)
   rope_table       the host-built table of TimestralForward.Plan.run (TimestralForward.java:599-610)
 """
@@ -41,6 +42,22 @@ def time_attention(qkv, out, key_valid, known, pos, table, gate, rows: int, enc:
     ctx = context(qkv.device.index or 0)
     _lib.call("jc_ts_time_attention", ctx.handle, _ptr(qkv), _ptr(out), _ptr(key_valid), _ptr(known), _ptr(pos),
               _ptr(table), _ptr(gate), rows, enc, ll, n, heads, dh, d, dt)
+
+
+def variate_attention(qkv, out, key_valid, group_start, group_end, role, covariates: bool, gate, rows: int,
+                      enc: int, n: int, heads: int, dh: int, d: int) -> None:
+    """Attention across the rows of each series per slot (TimestralKernels.variateAttention), scaled
+    by 1/sqrt(dh), under BlockLayout.variateAllowed; out *= sigmoid(gate) when gate is given.
+
+    qkv [rows*n, 3*d] and out (and gate) [rows*n, d] float32; key_valid int32 [rows*enc];
+    group_start/group_end int32 [rows] (contiguous groups); role int32 [rows] or None.
+    """
+    dt = _dtype_code(qkv)
+    if _dtype_code(out) != dt or (gate is not None and _dtype_code(gate) != dt):
+        raise _lib.JitcastArgumentError(_lib.JC_EINVAL, "qkv, out and gate must have the same dtype")
+    ctx = context(qkv.device.index or 0)
+    _lib.call("jc_ts_variate_attention", ctx.handle, _ptr(qkv), _ptr(out), _ptr(key_valid), _ptr(group_start),
+              _ptr(group_end), _ptr(role), int(bool(covariates)), _ptr(gate), rows, enc, n, heads, dh, d, dt)
 
 
 def gate(att, g) -> None:

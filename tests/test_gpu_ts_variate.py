@@ -1,0 +1,93 @@
+"""GPU parity of Timestral variate attention (BlockLayout.variateAllowed, 1/sqrt(dh) scale,
+optional sigmoid gate) against the C oracle, through the C ABI. Bar: max relative error <= 1e-4."""
+import numpy as np
+import pytest
+import torch
+
+from jitcast_amd import JitcastError, chronos2, rng, timestral
+from tests import cases
+
+pytestmark = pytest.mark.gpu
+TOL_F32 = 1e-4
+
+
+def _roles(seed, rows):
+    """TARGET 0 / PAST 1 / KNOWN 2 (BlockInput.java:35-37), seeded."""
+    return np.floor(rng.uniform(rng.stream_seed(seed, 6), rows) * 3).astype(np.int32)
+
+
+def _run(qkv, kv, group, role, cov, gate, rows, enc, n, heads, dh, d):
+    dev = torch.device("cuda:0")
+    s, e = chronos2.group_bounds(group)
+
+    def i32(a):
+        return torch.from_numpy(np.ascontiguousarray(a, np.int32).reshape(-1)).to(dev)
+
+    out = torch.full((rows * n, d), float("nan"), device=dev)
+    g = torch.from_numpy(gate).to(dev) if gate is not None else None
+    timestral.variate_attention(torch.from_numpy(qkv).to(dev), out, i32(kv), i32(s), i32(e), i32(role), cov, g, rows,
+                                enc, n, heads, dh, d)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+CASES = [
+    # rows, enc, h, heads, dh, d, group sizes lo..hi, covariates, valid probability, gate
+    (37, 6, 2, 2, 64, 128, 1, 8, 0, 0.7, False),
+    (64, 5, 3, 3, 64, 192, 1, 64, 1, 0.8, True),
+    (100, 4, 1, 2, 64, 128, 100, 100, 1, 0.9, False),  # one group larger than 64 rows
+    (45, 4, 2, 2, 32, 72, 1, 1, 0, 0.5, True),  # every row its own group
+    (50, 3, 2, 4, 16, 64, 5, 5, 1, 0.7, False),
+    (33, 2, 2, 2, 24, 48, 3, 20, 1, 0.6, True),  # dh not a multiple of 16
+    (20, 3, 1, 1, 128, 128, 20, 20, 1, 0.6, True),  # 128-wide heads
+    (17, 2, 0, 2, 48, 96, 17, 17, 0, 1.0, False),
+    (40, 0, 3, 2, 64, 128, 2, 9, 1, 1.0, False),  # decoder slots only
+]
+
+
+@pytest.mark.parametrize("rows,enc,h,heads,dh,d,lo,hi,cov,p,gate", CASES)
+def test_fp32_matches_oracle(gpu, oracle, rows, enc, h, heads, dh, d, lo, hi, cov, p, gate):
+    print(f"case rows={rows} enc={enc} h={h} heads={heads} dh={dh} groups {lo}..{hi} cov={cov} gate={gate}",
+          flush=True)
+    n = enc + h
+    qkv = cases.qkv(107, rows * n, d)
+    kv = cases.random_live(107, rows, max(enc, 1), p)[:, :enc].copy()
+    group = cases.group_sizes(107, rows, lo, hi)
+    role = _roles(107, rows) if cov else np.zeros(rows, np.int32)
+    g = cases.qkv(108, rows * n, d)[:, :d].copy() if gate else None
+    got = _run(qkv, kv, group, role, cov, g, rows, enc, n, heads, dh, d)[:, : heads * dh]
+    exp = oracle.ts_variate_attention(qkv, kv, group, role, cov, rows, enc, n, heads, dh, d)
+    if g is not None:
+        exp = oracle.ts_gate(exp, g)
+    exp = exp[:, : heads * dh]
+    assert np.isfinite(got).all()
+    err = oracle.rel_max_error(got, exp)
+    print(f"  rel err {err:.3e}", flush=True)
+    assert err <= TOL_F32
+
+
+def test_known_rows_never_read_other_rows(gpu, oracle):
+    """A group of known-covariate rows plus one target: perturbing the target's k/v leaves every
+    known row's output bit for bit (BlockLayout.java:236-238)."""
+    rows, enc, h, heads, dh, d = 6, 3, 1, 2, 64, 128
+    n = enc + h
+    qkv = cases.qkv(109, rows * n, d)
+    kv = np.ones((rows, enc), np.int32)
+    group = np.zeros(rows, np.int32)
+    role = np.array([0, 2, 2, 1, 2, 0], np.int32)
+    base = _run(qkv, kv, group, role, 1, None, rows, enc, n, heads, dh, d).reshape(rows, n, d)
+    p = qkv.copy().reshape(rows, n, 3 * d)
+    p[[0, 5], :, d:] += 2.0
+    pert = _run(p.reshape(rows * n, -1), kv, group, role, 1, None, rows, enc, n, heads, dh, d).reshape(rows, n, d)
+    np.testing.assert_array_equal(pert[[1, 2, 4]], base[[1, 2, 4]])
+    np.testing.assert_array_equal(pert[3], base[3])  # a PAST covariate never reads targets either
+    assert np.abs(pert[0] - base[0]).max() > 1e-3
+
+
+def test_bf16_is_not_built_yet(gpu):
+    dev = torch.device("cuda:0")
+    q = torch.zeros(4 * 3 * 64, dtype=torch.bfloat16, device=dev)
+    o = torch.zeros(4 * 64, dtype=torch.bfloat16, device=dev)
+    z = torch.zeros(4, dtype=torch.int32, device=dev)
+    with pytest.raises(JitcastError, match="not built"):
+        timestral.variate_attention(q, o, z, z, z + 1, None, False, None, 4, 1, 1, 1, 64, 64)
