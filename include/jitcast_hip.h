@@ -211,6 +211,25 @@ int jc_c2_group_order(const int32_t *group, int rows, int32_t *order, int *ident
  */
 int jc_c2_group_bounds(const int32_t *group, int rows, int32_t *start, int32_t *end);
 
+/*
+ * Timestral's block layout: BlockLayout.of and position() (J/timestral/BlockLayout.java:77-148,
+ * 203-207), host memory. The block runs the covariate path (*covariates_out = 1) when role is given,
+ * covariate_enabled is set and some row is not a TARGET; its window is then the context plus the
+ * horizon's known-future steps (future_observed [rows][h*patch], NULL = unobserved), so
+ * enc = t/patch + h, else enc = t/patch.
+ *   observed      [rows][t] 0/1, t a multiple of patch; h >= 1 (h <= block_size with covariates)
+ *   key_valid     out [rows*enc]: the patch has an observed step (attend_missing: or any earlier one)
+ *   known         out [rows]: the row is a KNOWN covariate of a covariate block
+ *   pos           out [rows*(enc+h)]: table row (position + enc) of every token, positions counted
+ *                 from the first patch any row of the series observes; decoder tokens continue from
+ *                 t/patch. Size key_valid and pos for enc = t/patch + h.
+ * Errors mirror BlockLayout.of's IllegalArgumentExceptions (JC_EINVAL).
+ */
+int jc_ts_block_layout(const uint8_t *observed, const uint8_t *future_observed, const int32_t *group,
+                       const int32_t *role, int rows, int t, int patch, int h, int covariate_enabled,
+                       int attend_missing, int block_size, int *enc_out, int *covariates_out, int32_t *key_valid,
+                       int32_t *known, int32_t *pos);
+
 #ifdef __cplusplus
 }
 #endif

@@ -65,6 +65,8 @@ SIGNATURES = {
     "jc_c2_live": (_i, [_vp, _i, _i, _i, _i, _i, _vp]),
     "jc_c2_group_order": (_i, [_vp, _i, _vp, _c.POINTER(_i)]),
     "jc_c2_group_bounds": (_i, [_vp, _i, _vp, _vp]),
+    "jc_ts_block_layout": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _c.POINTER(_i), _c.POINTER(_i), _vp,
+                                _vp, _vp]),
 }
 
 _lib = None

@@ -2,6 +2,7 @@
 // mask, the row order that makes groups contiguous and the per-row group bounds. The reference
 // computes these in Java on every forward call before uploading them (ModelLayout.java:70-116,
 // Chronos2Forward.java:147-194, 475-489; TimestralForward.java:614-629).
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <unordered_map>
@@ -73,6 +74,67 @@ int jc_c2_group_bounds(const int32_t* group, int rows, int32_t* start, int32_t* 
         }
         i = e;
     }
+    return JC_OK;
+}
+
+// BlockLayout.of (J/timestral/BlockLayout.java:77-148) and position() (203-207): the per-block
+// layout the Timestral attention kernels consume.
+int jc_ts_block_layout(const uint8_t* observed, const uint8_t* future_observed, const int32_t* group,
+                       const int32_t* role, int rows, int t, int patch, int h, int covariate_enabled,
+                       int attend_missing, int block_size, int* enc_out, int* covariates_out, int32_t* key_valid,
+                       int32_t* known, int32_t* pos) {
+    const char* W = "jc_ts_block_layout";
+    if (rows < 0 || t < 0 || patch < 1 || !enc_out || !covariates_out ||
+        (rows > 0 && (!observed || !group || !key_valid || !known || !pos)))
+        return jc::host_fail(JC_EINVAL, "%s: bad arguments (rows=%d t=%d patch=%d)", W, rows, t, patch);
+    if (t % patch != 0)
+        return jc::host_fail(JC_EINVAL, "%s: context length %d is not a multiple of the patch size %d", W, t, patch);
+    if (h < 1) return jc::host_fail(JC_EINVAL, "%s: horizon patches must be >= 1, got %d", W, h);
+    bool cov = false;
+    if (role && covariate_enabled)
+        for (int i = 0; i < rows; i++) cov |= role[i] != 0;
+    if (cov && h > block_size)
+        return jc::host_fail(JC_EINVAL, "%s: a block with covariates decodes at most %d patches, got %d", W,
+                             block_size, h);
+    const int ll = t / patch;
+    const int enc = cov ? ll + h : ll;
+    const int n = enc + h;
+    // the window's observation mask: the context, plus (with covariates) the known-future steps
+    auto obs = [&](int i, int s) -> bool {
+        if (s < t) return observed[(size_t)i * t + s] != 0;
+        return future_observed && future_observed[(size_t)i * h * patch + (s - t)] != 0;
+    };
+    std::vector<int> first_obs(rows, enc);
+    for (int i = 0; i < rows; i++) {
+        bool started = false;
+        for (int p = 0; p < enc; p++) {
+            bool any = false;
+            for (int s = p * patch; s < (p + 1) * patch; s++) any |= obs(i, s);
+            if (any && first_obs[i] == enc) first_obs[i] = p;
+            started |= any;
+            key_valid[(size_t)i * enc + p] = (attend_missing ? started : any) ? 1 : 0;
+        }
+    }
+    // the first patch any row of the series observes (0 if none does)
+    std::unordered_map<int32_t, int> group_first;
+    for (int i = 0; i < rows; i++) {
+        auto it = group_first.find(group[i]);
+        if (it == group_first.end())
+            group_first[group[i]] = first_obs[i];
+        else
+            it->second = std::min(it->second, first_obs[i]);
+    }
+    for (int i = 0; i < rows; i++) {
+        int f = group_first[group[i]];
+        f = f == enc ? 0 : f;
+        known[i] = (cov && role[i] == 2) ? 1 : 0;
+        for (int k = 0; k < n; k++) {
+            const int p = k < enc ? k : ll + k - enc;
+            pos[(size_t)i * n + k] = p - f + enc;  // the table row of jc_ts_rope_table
+        }
+    }
+    *enc_out = enc;
+    *covariates_out = cov ? 1 : 0;
     return JC_OK;
 }
 

@@ -60,6 +60,34 @@ def variate_attention(qkv, out, key_valid, group_start, group_end, role, covaria
               _ptr(group_end), _ptr(role), int(bool(covariates)), _ptr(gate), rows, enc, n, heads, dh, d, dt)
 
 
+def block_layout(observed, group, h: int, patch: int, role=None, future_observed=None, covariate_enabled=True,
+                 attend_missing=True, block_size: int = 1 << 30):
+    """BlockLayout.of (J/timestral/BlockLayout.java:77-148) on the host.
+
+    observed [rows, t] bool/0-1; group [rows]; role [rows] or None; future_observed [rows, h*patch]
+    or None. Returns (enc, covariates, key_valid [rows, enc], known [rows], pos [rows, enc+h]) with
+    pos holding table rows (position + enc) for time_attention.
+    """
+    obs = np.ascontiguousarray(observed, dtype=np.uint8)
+    rows, t = obs.shape
+    g = np.ascontiguousarray(group, dtype=np.int32)
+    r = None if role is None else np.ascontiguousarray(role, dtype=np.int32)
+    fut = None if future_observed is None else np.ascontiguousarray(future_observed, dtype=np.uint8)
+    enc_max = t // patch + h
+    kv = np.zeros(rows * enc_max, np.int32)
+    known = np.zeros(rows, np.int32)
+    pos = np.zeros(rows * (enc_max + h), np.int32)
+    enc, cov = ctypes.c_int(), ctypes.c_int()
+
+    def p(a):
+        return ctypes.c_void_p(0) if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+    _lib.call("jc_ts_block_layout", p(obs), p(fut), p(g), p(r), rows, t, patch, h, int(bool(covariate_enabled)),
+              int(bool(attend_missing)), block_size, ctypes.byref(enc), ctypes.byref(cov), p(kv), p(known), p(pos))
+    e = enc.value
+    return e, bool(cov.value), kv[: rows * e].reshape(rows, e), known, pos[: rows * (e + h)].reshape(rows, e + h)
+
+
 def gate(att, g) -> None:
     """att *= sigmoid(g), in place (TimestralKernels.gate)."""
     dt = _dtype_code(att)
