@@ -45,6 +45,7 @@ typedef enum jc_dtype {
 } jc_dtype;
 
 typedef struct jc_ctx jc_ctx;
+typedef struct jc_plan jc_plan;
 
 /* ---- runtime (replaces TornadoVM device selection and buffers: J/tornado/Devices.java:44-73) ---- */
 
@@ -72,6 +73,33 @@ int jc_device_info(jc_ctx *ctx, int *compute_units, char *arch, size_t arch_len)
 const char *jc_last_error(void);
 /* 1 + the library's ABI revision. */
 int jc_version(void);
+
+/* ---- plans: one captured hipGraph per batch shape (replaces a compiled TornadoVM execution plan:
+ *      J/tornado/PlanCache.java:40-161, J/chronos2/tornado/Chronos2Forward.java:106, 294-300) ------- */
+
+/*
+ * Starts capturing everything the context enqueues (attention entry points, device-to-device
+ * copies) into a plan for the batch shape `shape_key`. The context must launch on a created stream
+ * (jc_init's own, or one given to jc_set_stream), not the null stream. While capturing, host copies
+ * and jc_sync return JC_ESTATE: upload per-call inputs into the plan's buffers before
+ * jc_plan_launch, as the reference uploads them before each execution.
+ */
+int jc_plan_begin(jc_ctx *ctx, uint64_t shape_key);
+/* Ends the capture and instantiates the plan; on error no plan is made and capture has ended. */
+int jc_plan_end(jc_ctx *ctx, jc_plan **plan);
+/* Replays the plan on the context's current stream (asynchronous; jc_sync waits). */
+int jc_plan_launch(jc_plan *plan);
+/*
+ * Gives the plan ownership of a device buffer from jc_alloc: jc_plan_destroy frees it and
+ * jc_plan_device_bytes counts it, as each TornadoVM plan counts its own buffers (PlanCache.java:30-36).
+ */
+int jc_plan_adopt(jc_plan *plan, void *dptr, size_t bytes);
+/* The bytes of the buffers the plan owns. */
+int64_t jc_plan_device_bytes(jc_plan *plan);
+/* The shape key given to jc_plan_begin. */
+uint64_t jc_plan_key(jc_plan *plan);
+/* Waits for the plan's stream, frees the adopted buffers and the graph (idempotent on NULL). */
+int jc_plan_destroy(jc_plan *plan);
 
 /* ---- synthetic inputs (no reference counterpart: the benchmark's seeded generator) ---------------- */
 

@@ -9,6 +9,6 @@ from ._lib import JitcastArgumentError, JitcastError, LibraryMissing
 
 _lib.lib()
 
-from . import chronos2, rng, runtime, timestral  # noqa: E402
+from . import chronos2, plans, rng, runtime, timestral  # noqa: E402
 
-__all__ = ["chronos2", "timestral", "rng", "runtime", "JitcastError", "JitcastArgumentError", "LibraryMissing"]
+__all__ = ["chronos2", "timestral", "plans", "rng", "runtime", "JitcastError", "JitcastArgumentError", "LibraryMissing"]

@@ -53,6 +53,13 @@ SIGNATURES = {
     "jc_device_info": (_i, [_vp, _c.POINTER(_i), _c.c_char_p, _sz]),
     "jc_last_error": (_c.c_char_p, []),
     "jc_version": (_i, []),
+    "jc_plan_begin": (_i, [_vp, _c.c_uint64]),
+    "jc_plan_end": (_i, [_vp, _c.POINTER(_vp)]),
+    "jc_plan_launch": (_i, [_vp]),
+    "jc_plan_adopt": (_i, [_vp, _vp, _sz]),
+    "jc_plan_device_bytes": (_c.c_int64, [_vp]),
+    "jc_plan_key": (_c.c_uint64, [_vp]),
+    "jc_plan_destroy": (_i, [_vp]),
     "jc_fill_normal": (_i, [_vp, _vp, _c.c_uint64, _c.c_uint64, _f, _f]),
     "jc_fill_uniform": (_i, [_vp, _vp, _c.c_uint64, _c.c_uint64, _f, _f]),
     "jc_c2_rope_table": (_i, [_i, _i, _f, _vp]),

@@ -20,6 +20,17 @@ struct jc_ctx {
     hipStream_t stream;  // where launches go (own, or a caller's)
     int cus;
     char arch[64];
+    bool capturing;          // between jc_plan_begin and jc_plan_end
+    hipStream_t capture_on;  // the stream being captured
+    uint64_t capture_key;
+};
+
+struct jc_plan {
+    jc_ctx* ctx;
+    hipGraph_t graph;
+    hipGraphExec_t exec;
+    uint64_t key;
+    std::vector<std::pair<void*, size_t>> owned;  // device buffers adopted by the plan
 };
 
 namespace {
@@ -93,6 +104,9 @@ int jc_init(int device, jc_ctx** out) {
         return hip_fail("jc_init: hipStreamCreate", e);
     }
     ctx->stream = ctx->own;
+    ctx->capturing = false;
+    ctx->capture_on = nullptr;
+    ctx->capture_key = 0;
     *out = ctx;
     return JC_OK;
 }
@@ -100,6 +114,11 @@ int jc_init(int device, jc_ctx** out) {
 int jc_destroy(jc_ctx* ctx) {
     if (!ctx) return JC_OK;
     (void)hipSetDevice(ctx->device);
+    if (ctx->capturing) {
+        hipGraph_t g = nullptr;
+        if (hipStreamEndCapture(ctx->capture_on, &g) == hipSuccess && g) (void)hipGraphDestroy(g);
+        ctx->capturing = false;
+    }
     (void)hipStreamSynchronize(ctx->stream);
     (void)hipStreamDestroy(ctx->own);
     delete ctx;
@@ -108,6 +127,8 @@ int jc_destroy(jc_ctx* ctx) {
 
 int jc_set_stream(jc_ctx* ctx, void* stream) {
     if (!ctx) return fail(JC_EINVAL, "jc_set_stream: null context");
+    if (ctx->capturing && (hipStream_t)stream != ctx->capture_on)
+        return fail(JC_ESTATE, "jc_set_stream: the context is capturing a plan on another stream");
     ctx->stream = (hipStream_t)stream;  // NULL is the device's default (null) stream
     return JC_OK;
 }
@@ -140,6 +161,8 @@ int jc_free(jc_ctx* ctx, void* dptr) {
 static int copy(jc_ctx* ctx, void* dst, const void* src, size_t bytes, hipMemcpyKind kind, const char* where) {
     int rc = use(ctx, where);
     if (rc) return rc;
+    if (ctx->capturing && kind != hipMemcpyDeviceToDevice)
+        return fail(JC_ESTATE, "%s: host copies cannot be captured into a plan (upload before jc_plan_begin)", where);
     if (bytes == 0) return JC_OK;
     if (!dst || !src) return fail(JC_EINVAL, "%s: null pointer", where);
     hipError_t e = hipMemcpyAsync(dst, src, bytes, kind, ctx->stream);
@@ -165,6 +188,7 @@ int jc_memcpy_d2d(jc_ctx* ctx, void* dst, const void* src, size_t bytes) {
 int jc_sync(jc_ctx* ctx) {
     int rc = use(ctx, "jc_sync");
     if (rc) return rc;
+    if (ctx->capturing) return fail(JC_ESTATE, "jc_sync: the context is capturing a plan");
     hipError_t e = hipStreamSynchronize(ctx->stream);
     return e == hipSuccess ? JC_OK : hip_fail("jc_sync", e);
 }
@@ -407,6 +431,102 @@ int jc_ts_variate_attention(jc_ctx* ctx, const void* qkv, void* out, const int32
     a.qscale = (float)(1.4426950408889634 / std::sqrt((double)dh));
     hipError_t e = jc::group_attention_f32_launch(a, dh, true, ctx->stream);
     return e == hipSuccess ? JC_OK : hip_fail(W, e);
+}
+
+// ---- plans: one captured hipGraph per batch shape ----------------------------------------------
+
+int jc_plan_begin(jc_ctx* ctx, uint64_t shape_key) {
+    const char* W = "jc_plan_begin";
+    int rc = use(ctx, W);
+    if (rc) return rc;
+    if (ctx->capturing) return fail(JC_ESTATE, "%s: a plan is already being captured", W);
+    if (ctx->stream == nullptr)
+        return fail(JC_ESTATE, "%s: the null stream cannot be captured (jc_set_stream a created stream)", W);
+    hipError_t e = hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal);
+    if (e != hipSuccess) return hip_fail(W, e);
+    ctx->capturing = true;
+    ctx->capture_on = ctx->stream;
+    ctx->capture_key = shape_key;
+    return JC_OK;
+}
+
+int jc_plan_end(jc_ctx* ctx, jc_plan** out) {
+    const char* W = "jc_plan_end";
+    if (!out) return fail(JC_EINVAL, "%s: null output pointer", W);
+    *out = nullptr;
+    int rc = use(ctx, W);
+    if (rc) return rc;
+    if (!ctx->capturing) return fail(JC_ESTATE, "%s: no plan is being captured", W);
+    ctx->capturing = false;
+    hipGraph_t graph = nullptr;
+    hipError_t e = hipStreamEndCapture(ctx->capture_on, &graph);
+    if (e != hipSuccess) {
+        if (graph) (void)hipGraphDestroy(graph);
+        return hip_fail(W, e);
+    }
+    hipGraphExec_t exec = nullptr;
+    e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        (void)hipGraphDestroy(graph);
+        return hip_fail("jc_plan_end: hipGraphInstantiate", e);
+    }
+    jc_plan* plan = new (std::nothrow) jc_plan();
+    if (!plan) {
+        (void)hipGraphExecDestroy(exec);
+        (void)hipGraphDestroy(graph);
+        return fail(JC_ENOMEM, "%s: out of host memory", W);
+    }
+    plan->ctx = ctx;
+    plan->graph = graph;
+    plan->exec = exec;
+    plan->key = ctx->capture_key;
+    *out = plan;
+    return JC_OK;
+}
+
+int jc_plan_launch(jc_plan* plan) {
+    if (!plan) return fail(JC_EINVAL, "jc_plan_launch: null plan");
+    int rc = use(plan->ctx, "jc_plan_launch");
+    if (rc) return rc;
+    if (plan->ctx->capturing) return fail(JC_ESTATE, "jc_plan_launch: the context is capturing a plan");
+    hipError_t e = hipGraphLaunch(plan->exec, plan->ctx->stream);
+    return e == hipSuccess ? JC_OK : hip_fail("jc_plan_launch", e);
+}
+
+int jc_plan_adopt(jc_plan* plan, void* dptr, size_t bytes) {
+    if (!plan) return fail(JC_EINVAL, "jc_plan_adopt: null plan");
+    if (!dptr) return fail(JC_EINVAL, "jc_plan_adopt: null device pointer");
+    try {
+        plan->owned.emplace_back(dptr, bytes);
+    } catch (...) {
+        return fail(JC_ENOMEM, "jc_plan_adopt: out of host memory");
+    }
+    return JC_OK;
+}
+
+int64_t jc_plan_device_bytes(jc_plan* plan) {
+    if (!plan) return 0;
+    int64_t total = 0;
+    for (const auto& b : plan->owned) total += (int64_t)b.second;
+    return total;
+}
+
+uint64_t jc_plan_key(jc_plan* plan) { return plan ? plan->key : 0; }
+
+int jc_plan_destroy(jc_plan* plan) {
+    if (!plan) return JC_OK;
+    (void)hipSetDevice(plan->ctx->device);
+    int rc = JC_OK;
+    hipError_t e = hipStreamSynchronize(plan->ctx->stream);  // the graph may still be running
+    if (e != hipSuccess) rc = hip_fail("jc_plan_destroy", e);
+    (void)hipGraphExecDestroy(plan->exec);
+    (void)hipGraphDestroy(plan->graph);
+    for (const auto& b : plan->owned) {
+        e = hipFree(b.first);
+        if (e != hipSuccess && rc == JC_OK) rc = hip_fail("jc_plan_destroy: hipFree", e);
+    }
+    delete plan;
+    return rc;
 }
 
 }  // extern "C"
