@@ -8,6 +8,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <new>
 #include <vector>
@@ -60,6 +61,13 @@ int use(jc_ctx* ctx, const char* where) {
 }
 
 size_t dtype_size(int dtype) { return dtype == JC_F32 ? 4 : 2; }
+
+// JITCAST_HIP_LPW=1 sends bf16/fp16 rows that fit it to the row-wide kernel (read at every launch, so
+// a host can switch between the kernels at run time)
+bool lpw_enabled() {
+    const char* e = getenv("JITCAST_HIP_LPW");
+    return e && e[0] == '1';
+}
 
 }  // namespace
 
@@ -265,9 +273,18 @@ static int check_time_common(const char* W, const void* qkv, const void* out, co
     return JC_OK;
 }
 
+// fp32 goes to the fp32 kernel; bf16/fp16 to the streaming kernel, or to the row-wide one when asked
+// for and the shape fits it (both give the same results to within rounding; neither is faster on
+// every shape).
 static int launch_time(jc_ctx* ctx, const char* W, const jc::TimeArgs& a, int dh, bool ts, int dtype) {
-    hipError_t e = dtype == JC_F32 ? jc::time_attention_f32_launch(a, dh, ts, ctx->stream)
-                                   : jc::time_attention_lp_launch(a, dh, ts, dtype == JC_F16, ctx->stream);
+    hipError_t e;
+    if (dtype == JC_F32) {
+        e = jc::time_attention_f32_launch(a, dh, ts, ctx->stream);
+    } else if (lpw_enabled() && jc::time_attention_lpw_fits(a, dh)) {
+        e = jc::time_attention_lpw_launch(a, dh, ts, dtype == JC_F16, ctx->stream);
+    } else {
+        e = jc::time_attention_lp_launch(a, dh, ts, dtype == JC_F16, ctx->stream);
+    }
     return e == hipSuccess ? JC_OK : hip_fail(W, e);
 }
 

@@ -14,6 +14,10 @@ namespace jc {
 hipError_t time_attention_f32_launch(const TimeArgs& a, int dh, bool ts, hipStream_t stream);
 hipError_t time_attention_lp_launch(const TimeArgs& a, int dh, bool ts, bool fp16, hipStream_t stream);
 int time_attention_max_tokens();
+// The row-wide bf16/fp16 kernel: 8-wave workgroups of 256 queries of one (row, head); dh 32 or 64;
+// rows of at least 256 tokens.
+bool time_attention_lpw_fits(const TimeArgs& a, int dh);
+hipError_t time_attention_lpw_launch(const TimeArgs& a, int dh, bool ts, bool fp16, hipStream_t stream);
 // att[i] *= sigmoid(g[i]) for i < count (dtype: 0 fp32, 1 bf16, 2 fp16)
 hipError_t gate_launch(void* att, const void* g, uint64_t count, int dtype, hipStream_t stream);
 // The arguments of the group-attention kernels (by value).

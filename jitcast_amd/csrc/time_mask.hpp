@@ -40,6 +40,7 @@ struct TimeArgs {
     int table_rows;         // rows of the table a pos value may address
     float qscale;           // score scale times log2(e), folded into q
     int qgroups;            // workgroups per (row, head)
+    int q_begin;            // the first query the launch covers (0: all of them)
 };
 
 template <bool TS>
