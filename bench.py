@@ -102,7 +102,7 @@ def group_attention_line(steps: int, warmup: int) -> dict:
     log(f"group attention: {ms:.4f} ms, {gbs:.0f} GB/s algorithmic ({100 * gbs / PEAK_HBM_GBS:.1f}% of HBM)")
     res = {
         "workload": "config 2: fp32 Chronos-2 group attention, 4096 rows x 129 slots, 12x64, groups U{1..64}",
-        "kernel": "c2_group_attention_f32<64>",
+        "kernel": "jc::group_attention_f32<64, false, true>",
         "launch_ms": round(ms, 5),
         "value": round(gbs, 1),
         "unit": "GB/s",
@@ -137,7 +137,7 @@ def time_attention_lowp_line(case, steps: int, warmup: int, dtype_name: str) -> 
         f"({100 * tf / PEAK_BF16_TFLOPS:.1f}% of the {dtype_name} MFMA peak)")
     res = {
         "workload": f"config 1-{dtype_name}: the config-1 inputs with qkv in {dtype_name}, fp32 accumulation",
-        "kernel": f"c2_time_attention_lp<{dtype_name},64>",
+        "kernel": "jc::time_attention_lp<%s, 64, 4, true, false, true>" % {"bf16": "__bf16", "fp16": "_Float16"}[dtype_name],
         "launch_ms": round(ms, 5),
         "value": round(tf, 2),
         "unit": "TFLOP/s",
@@ -265,7 +265,7 @@ def main() -> int:
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_FP32_TFLOPS, 4),
             "traffic": traffic_from_profile("c2_time_attention_f32_config1"),
-            "kernel": "c2_time_attention_f32<64>",
+            "kernel": "jc::time_attention_f32<64, 32, true, false, true>",
             "launch_ms": round(launch_ms, 5),
         },
         "cpu_baseline": cpu,
