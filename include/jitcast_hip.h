@@ -258,6 +258,73 @@ int jc_ts_block_layout(const uint8_t *observed, const uint8_t *future_observed, 
                        int attend_missing, int block_size, int *enc_out, int *covariates_out, int32_t *key_valid,
                        int32_t *known, int32_t *pos);
 
+/* ---- The Chronos-2 encoder layer around the attention cores (fp32) -------------------------- */
+
+/* Kernels.gemm flags (J/tornado/Kernels.java:50-56). */
+#define JC_GEMM_BIAS 1
+#define JC_GEMM_ACCUMULATE 2
+#define JC_GEMM_SILU 4
+#define JC_GEMM_RELU 16
+
+/*
+ * C[m, n] (+)= act(A[m, :k] . W[n, :k] + bias[n]), fp32 on MFMA, in the epilogue order bias,
+ * activation (SILU or RELU), accumulate. Replaces Kernels.gemm / gemmBlocked / gemmBlockedWide and
+ * the cuBLAS path of Chronos2Forward.Plan.gemm (J/tornado/Kernels.java:59-103, 233-480;
+ * J/chronos2/tornado/Chronos2Forward.java:312-409); W is PyTorch's [out, in]. A non-NULL bias sets
+ * JC_GEMM_BIAS, as Plan.gemm does for a Lin with a bias.
+ *   a [m, lda], w [n, k], c [m, ldc] device fp32; k a multiple of 16, lda >= k and a multiple of 4,
+ *   ldc >= n; a and w 16-byte aligned.
+ */
+int jc_linear(jc_ctx *ctx, const float *a, int lda, const float *w, const float *bias, float *c, int ldc, int m,
+              int n, int k, int flags);
+
+/*
+ * y = x * (1 / sqrt(mean(x^2) + eps)) * w per row of d: Kernels.rmsNorm (J/tornado/Kernels.java:800-829)
+ * and Ops.rmsNorm (J/cpu/Ops.java:53-68). x, y [rows, d] device fp32 (may alias), w [d] or NULL;
+ * d a multiple of 4; 16-byte aligned.
+ */
+int jc_rms_norm(jc_ctx *ctx, const float *x, const float *w, float *y, int rows, int d, float eps);
+
+/* Device weights of one Chronos-2 encoder layer (Chronos2Packed.Layer, Chronos2Packed.java:41-47,
+ * 150-154); a bias pointer may be NULL (no bias). */
+typedef struct jc_c2_layer_weights {
+    const float *time_norm;  /* [d] */
+    const float *time_qkv;   /* [3*inner, d]: q | k | v rows, heads-major */
+    const float *time_qkv_bias;
+    const float *time_o;     /* [d, inner] */
+    const float *time_o_bias;
+    const float *group_norm; /* [d] */
+    const float *group_qkv;  /* [3*inner, d] */
+    const float *group_qkv_bias;
+    const float *group_o;    /* [d, inner] */
+    const float *group_o_bias;
+    const float *mlp_norm;   /* [d] */
+    const float *wi;         /* [dff, d] */
+    const float *wi_bias;
+    const float *wo;         /* [d, dff] */
+    const float *wo_bias;
+} jc_c2_layer_weights;
+
+/* Bytes of the workspace jc_c2_layer needs (hn [T, d], big [T, max(3*inner, dff)], att [T, inner]
+ * floats for T = rows*n tokens, each part 256-byte aligned), or -1 for a negative size. */
+int64_t jc_c2_layer_workspace_bytes(int rows, int n, int d, int inner, int dff);
+
+/*
+ * One Chronos-2 encoder layer in place on x [rows*n, d] (the per-layer stage of
+ * Chronos2Forward.Plan, J/chronos2/tornado/Chronos2Forward.java:258-286; CPU CpuChronos2.forward,
+ * J/chronos2/cpu/CpuChronos2.java:150-161):
+ *   x += O_time(timeAttention(RoPE(QKV_time(rmsNorm(x)))))
+ *   x += O_group(groupAttention(QKV_group(rmsNorm(x))))
+ *   x += Wo(ReLU(Wi(rmsNorm(x))))
+ * live [rows*n], table [n, dh] (jc_c2_rope_table), group_start/group_end [rows] as for
+ * jc_c2_time_attention and jc_c2_group_attention (groups contiguous); workspace of
+ * jc_c2_layer_workspace_bytes, 256-byte aligned. inner = heads*dh. d a multiple of 16, dh a multiple
+ * of 16 and at most 64, dff a multiple of 16.
+ */
+int jc_c2_layer(jc_ctx *ctx, float *x, const jc_c2_layer_weights *w, const int32_t *live, const float *table,
+                const int32_t *group_start, const int32_t *group_end, void *workspace, int rows, int n, int d,
+                int heads, int dh, int dff, float eps);
+
 #ifdef __cplusplus
 }
 #endif

@@ -72,6 +72,10 @@ SIGNATURES = {
     "jc_c2_live": (_i, [_vp, _i, _i, _i, _i, _i, _vp]),
     "jc_c2_group_order": (_i, [_vp, _i, _vp, _c.POINTER(_i)]),
     "jc_c2_group_bounds": (_i, [_vp, _i, _vp, _vp]),
+    "jc_linear": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _i]),
+    "jc_rms_norm": (_i, [_vp, _vp, _vp, _vp, _i, _i, _f]),
+    "jc_c2_layer_workspace_bytes": (_c.c_int64, [_i, _i, _i, _i, _i]),
+    "jc_c2_layer": (_i, [_vp, _vp, _vp, _i32p, _vp, _i32p, _i32p, _vp, _i, _i, _i, _i, _i, _i, _f]),
     "jc_ts_block_layout": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _c.POINTER(_i), _c.POINTER(_i), _vp,
                                 _vp, _vp]),
 }

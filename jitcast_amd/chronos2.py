@@ -8,6 +8,10 @@ on the GPU, and launches on torch's current stream:
   group_attention  Chronos2Kernels.groupAttention (Chronos2Kernels.java:473-474)
   rope_table       the host-built table of Chronos2Forward.Plan.run (Chronos2Forward.java:465-474)
   live_mask, group_order, group_bounds   ModelLayout.java:104-114, Chronos2Forward.java:178-194, 475-489
+  linear           Kernels.gemm and its flags (J/tornado/Kernels.java:50-103), as Chronos2Forward.Plan.gemm
+                   calls it (Chronos2Forward.java:312-369)
+  rms_norm         Kernels.rmsNorm (Kernels.java:800-829)
+  layer            one encoder layer: the per-layer stage of Chronos2Forward.Plan (Chronos2Forward.java:258-286)
 """
 from __future__ import annotations
 
@@ -95,3 +99,70 @@ def group_bounds(group) -> tuple[np.ndarray, np.ndarray]:
     _lib.call("jc_c2_group_bounds", g.ctypes.data_as(ctypes.c_void_p), len(g), start.ctypes.data_as(ctypes.c_void_p),
               end.ctypes.data_as(ctypes.c_void_p))
     return start, end
+
+
+GEMM_BIAS, GEMM_ACCUMULATE, GEMM_SILU, GEMM_RELU = 1, 2, 4, 16
+
+
+def _f32(t, name):
+    if str(t.dtype) != "torch.float32":
+        raise _lib.JitcastArgumentError(_lib.JC_EINVAL, f"{name} must be float32")
+
+
+def linear(a, w, c, bias=None, flags: int = 0, m: int | None = None, n: int | None = None, k: int | None = None,
+           lda: int | None = None, ldc: int | None = None) -> None:
+    """c (+)= act(a . w^T + bias) on torch's current stream; w is [n, k] (PyTorch's Linear layout).
+
+    flags: GEMM_ACCUMULATE, GEMM_RELU, GEMM_SILU (GEMM_BIAS is implied by a bias). Sizes default to
+    the tensors' shapes: a [m, k] (row stride lda), c [m, n] (row stride ldc).
+    """
+    for t, nm in ((a, "a"), (w, "w"), (c, "c")):
+        _f32(t, nm)
+    m = a.shape[0] if m is None else m
+    n = w.shape[0] if n is None else n
+    k = w.shape[1] if k is None else k
+    lda = a.stride(0) if lda is None else lda
+    ldc = c.stride(0) if ldc is None else ldc
+    ctx = context(a.device.index or 0)
+    _lib.call("jc_linear", ctx.handle, _ptr(a), lda, _ptr(w), _ptr(bias), _ptr(c), ldc, m, n, k, flags)
+
+
+def rms_norm(x, w, y, eps: float) -> None:
+    """y = x * (1 / sqrt(mean(x^2) + eps)) * w per row; x, y [rows, d] float32 (may be the same tensor)."""
+    _f32(x, "x")
+    _f32(y, "y")
+    ctx = context(x.device.index or 0)
+    rows, d = x.shape
+    _lib.call("jc_rms_norm", ctx.handle, _ptr(x), _ptr(w), _ptr(y), rows, d, ctypes.c_float(eps))
+
+
+class LayerWeights(ctypes.Structure):
+    """jc_c2_layer_weights: device pointers of one encoder layer (Chronos2Packed.Layer)."""
+
+    _fields_ = [(name, ctypes.c_void_p) for name in (
+        "time_norm", "time_qkv", "time_qkv_bias", "time_o", "time_o_bias",
+        "group_norm", "group_qkv", "group_qkv_bias", "group_o", "group_o_bias",
+        "mlp_norm", "wi", "wi_bias", "wo", "wo_bias")]
+
+    @classmethod
+    def of(cls, tensors: dict) -> "LayerWeights":
+        """From a dict of float32 device tensors keyed by field name (missing biases are NULL)."""
+        lw = cls()
+        for name, _ in cls._fields_:
+            t = tensors.get(name)
+            setattr(lw, name, t.data_ptr() if t is not None else None)
+        return lw
+
+
+def layer_workspace_bytes(rows: int, n: int, d: int, inner: int, dff: int) -> int:
+    return int(_lib.lib().jc_c2_layer_workspace_bytes(rows, n, d, inner, dff))
+
+
+def layer(x, weights: dict, live, table, group_start, group_end, workspace, rows: int, n: int, d: int, heads: int,
+          dh: int, dff: int, eps: float) -> None:
+    """One Chronos-2 encoder layer in place on x [rows*n, d] float32 (see include/jitcast_hip.h)."""
+    _f32(x, "x")
+    ctx = context(x.device.index or 0)
+    lw = LayerWeights.of(weights)
+    _lib.call("jc_c2_layer", ctx.handle, _ptr(x), ctypes.byref(lw), _ptr(live), _ptr(table), _ptr(group_start),
+              _ptr(group_end), _ptr(workspace), rows, n, d, heads, dh, dff, ctypes.c_float(eps))

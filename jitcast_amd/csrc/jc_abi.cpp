@@ -546,4 +546,112 @@ int jc_plan_destroy(jc_plan* plan) {
     return rc;
 }
 
+
+// ---- The Chronos-2 encoder layer around the attention cores ----------------------------------
+
+static int check_linear(const char* W, const float* a, int lda, const float* w, const float* bias, const float* c,
+                        int ldc, int m, int n, int k, int flags) {
+    if (m < 0 || n < 0 || k < 0) return fail(JC_EINVAL, "%s: negative size (m=%d n=%d k=%d)", W, m, n, k);
+    if ((size_t)m * n == 0) return JC_OK;
+    if (!a || !w || !c) return fail(JC_EINVAL, "%s: null a, w or c", W);
+    if (k % 16) return fail(JC_EINVAL, "%s: k must be a multiple of 16 (got %d)", W, k);
+    if (lda < k || lda % 4) return fail(JC_EINVAL, "%s: lda must be >= k and a multiple of 4 (got %d)", W, lda);
+    if (ldc < n) return fail(JC_EINVAL, "%s: ldc must be >= n (got %d)", W, ldc);
+    if (!aligned16(a) || !aligned16(w)) return fail(JC_EINVAL, "%s: a and w must be 16-byte aligned", W);
+    if (flags & ~(JC_GEMM_BIAS | JC_GEMM_ACCUMULATE | JC_GEMM_SILU | JC_GEMM_RELU))
+        return fail(JC_EINVAL, "%s: unknown flags 0x%x", W, flags);
+    if ((flags & JC_GEMM_SILU) && (flags & JC_GEMM_RELU)) return fail(JC_EINVAL, "%s: SILU and RELU together", W);
+    if ((flags & JC_GEMM_BIAS) && !bias) return fail(JC_EINVAL, "%s: JC_GEMM_BIAS without a bias", W);
+    return JC_OK;
+}
+
+static int launch_linear(jc_ctx* ctx, const char* W, const float* a, int lda, const float* w, const float* bias,
+                         float* c, int ldc, int m, int n, int k, int flags) {
+    if (bias) flags |= JC_GEMM_BIAS;
+    int rc = check_linear(W, a, lda, w, bias, c, ldc, m, n, k, flags);
+    if (rc || (size_t)m * n == 0) return rc;
+    jc::GemmArgs g{a, w, bias, c, m, n, k, lda, ldc, flags};
+    hipError_t e = jc::gemm_f32_launch(g, ctx->stream);
+    return e == hipSuccess ? JC_OK : hip_fail(W, e);
+}
+
+int jc_linear(jc_ctx* ctx, const float* a, int lda, const float* w, const float* bias, float* c, int ldc, int m, int n,
+              int k, int flags) {
+    const char* W = "jc_linear";
+    int rc = use(ctx, W);
+    if (rc) return rc;
+    return launch_linear(ctx, W, a, lda, w, bias, c, ldc, m, n, k, flags);
+}
+
+static int launch_rms(jc_ctx* ctx, const char* W, const float* x, const float* w, float* y, int rows, int d, float eps) {
+    if (rows < 0 || d < 0) return fail(JC_EINVAL, "%s: negative size", W);
+    if ((size_t)rows * d == 0) return JC_OK;
+    if (!x || !y) return fail(JC_EINVAL, "%s: null x or y", W);
+    if (d % 4) return fail(JC_EINVAL, "%s: d must be a multiple of 4 (got %d)", W, d);
+    if (!aligned16(x) || !aligned16(y) || (w && !aligned16(w))) return fail(JC_EINVAL, "%s: 16-byte alignment", W);
+    hipError_t e = jc::rms_norm_f32_launch(x, y, w, rows, d, eps, ctx->stream);
+    return e == hipSuccess ? JC_OK : hip_fail(W, e);
+}
+
+int jc_rms_norm(jc_ctx* ctx, const float* x, const float* w, float* y, int rows, int d, float eps) {
+    const char* W = "jc_rms_norm";
+    int rc = use(ctx, W);
+    if (rc) return rc;
+    return launch_rms(ctx, W, x, w, y, rows, d, eps);
+}
+
+static size_t round256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+int64_t jc_c2_layer_workspace_bytes(int rows, int n, int d, int inner, int dff) {
+    if (rows < 0 || n < 0 || d < 0 || inner < 0 || dff < 0) return -1;
+    const size_t t = (size_t)rows * n;
+    const size_t big = (size_t)(3 * inner > dff ? 3 * inner : dff);
+    return (int64_t)(round256(t * d * 4) + round256(t * big * 4) + round256(t * (size_t)inner * 4));
+}
+
+int jc_c2_layer(jc_ctx* ctx, float* x, const jc_c2_layer_weights* w, const int32_t* live, const float* table,
+                const int32_t* group_start, const int32_t* group_end, void* workspace, int rows, int n, int d, int heads,
+                int dh, int dff, float eps) {
+    const char* W = "jc_c2_layer";
+    int rc = use(ctx, W);
+    if (rc) return rc;
+    if (rows < 0 || n < 0 || d <= 0 || heads <= 0 || dh <= 0 || dff <= 0)
+        return fail(JC_EINVAL, "%s: sizes must be positive (rows=%d n=%d d=%d heads=%d dh=%d dff=%d)", W, rows, n, d,
+                    heads, dh, dff);
+    if ((size_t)rows * n == 0) return JC_OK;
+    if (!x || !w || !workspace) return fail(JC_EINVAL, "%s: null x, weights or workspace", W);
+    if (d % 16 || dff % 16 || dh % 16 || dh > 64)
+        return fail(JC_EINVAL, "%s: d and dff must be multiples of 16, dh a multiple of 16 up to 64 (d=%d dff=%d dh=%d)",
+                    W, d, dff, dh);
+    if (((uintptr_t)workspace & 255u) != 0) return fail(JC_EINVAL, "%s: workspace must be 256-byte aligned", W);
+    if (!w->time_norm || !w->time_qkv || !w->time_o || !w->group_norm || !w->group_qkv || !w->group_o ||
+        !w->mlp_norm || !w->wi || !w->wo)
+        return fail(JC_EINVAL, "%s: a null weight matrix or norm", W);
+    const int inner = heads * dh, T = rows * n;
+    const size_t big_cols = (size_t)(3 * inner > dff ? 3 * inner : dff);
+    char* ws = static_cast<char*>(workspace);
+    float* hn = reinterpret_cast<float*>(ws);
+    float* big = reinterpret_cast<float*>(ws + round256((size_t)T * d * 4));  // qkv [T, 3*inner] or act [T, dff]
+    float* att = reinterpret_cast<float*>(ws + round256((size_t)T * d * 4) + round256((size_t)T * big_cols * 4));
+
+    // time attention sub-layer (Chronos2Forward.java:260-271)
+    if ((rc = launch_rms(ctx, W, x, w->time_norm, hn, T, d, eps))) return rc;
+    if ((rc = launch_linear(ctx, W, hn, d, w->time_qkv, w->time_qkv_bias, big, 3 * inner, T, 3 * inner, d, 0))) return rc;
+    if ((rc = jc_c2_time_attention(ctx, big, att, live, table, rows, n, heads, dh, inner, JC_F32))) return rc;
+    if ((rc = launch_linear(ctx, W, att, inner, w->time_o, w->time_o_bias, x, d, T, d, inner, JC_GEMM_ACCUMULATE)))
+        return rc;
+    // group attention sub-layer (Chronos2Forward.java:273-281)
+    if ((rc = launch_rms(ctx, W, x, w->group_norm, hn, T, d, eps))) return rc;
+    if ((rc = launch_linear(ctx, W, hn, d, w->group_qkv, w->group_qkv_bias, big, 3 * inner, T, 3 * inner, d, 0)))
+        return rc;
+    if ((rc = jc_c2_group_attention(ctx, big, att, live, group_start, group_end, rows, n, heads, dh, inner, JC_F32)))
+        return rc;
+    if ((rc = launch_linear(ctx, W, att, inner, w->group_o, w->group_o_bias, x, d, T, d, inner, JC_GEMM_ACCUMULATE)))
+        return rc;
+    // feed-forward sub-layer (Chronos2Forward.java:283-286)
+    if ((rc = launch_rms(ctx, W, x, w->mlp_norm, hn, T, d, eps))) return rc;
+    if ((rc = launch_linear(ctx, W, hn, d, w->wi, w->wi_bias, big, dff, T, dff, d, JC_GEMM_RELU))) return rc;
+    return launch_linear(ctx, W, big, dff, w->wo, w->wo_bias, x, d, T, d, dff, JC_GEMM_ACCUMULATE);
+}
+
 }  // extern "C"

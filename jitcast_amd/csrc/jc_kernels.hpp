@@ -45,4 +45,18 @@ hipError_t fill_normal_launch(float* out, uint64_t count, uint64_t stream_seed, 
 hipError_t fill_uniform_launch(float* out, uint64_t count, uint64_t stream_seed, double lo, double hi,
                                hipStream_t stream);
 
+// C[m, n] (+)= act(A[m, :k] . W[n, :k] + b[n]) in fp32 (Kernels.gemm's flags, Kernels.java:50-56).
+constexpr int kGemmBias = 1, kGemmAccumulate = 2, kGemmSilu = 4, kGemmRelu = 16;
+struct GemmArgs {
+    const float* a;     // [m, lda]
+    const float* w;     // [n, k]
+    const float* bias;  // [n] when flags & kGemmBias
+    float* c;           // [m, ldc]
+    int m, n, k, lda, ldc, flags;
+};
+// k a multiple of 16; lda a multiple of 4; a, w 16-byte aligned
+hipError_t gemm_f32_launch(const GemmArgs& g, hipStream_t stream);
+// y = x * (1 / sqrt(mean(x^2) + eps)) * w per row of d (d a multiple of 4; w may be null)
+hipError_t rms_norm_f32_launch(const float* x, float* y, const float* w, int rows, int d, float eps, hipStream_t stream);
+
 }  // namespace jc

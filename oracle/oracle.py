@@ -153,6 +153,38 @@ def rms_norm(x, w, eps) -> np.ndarray:
     return y
 
 
+def relu(x) -> np.ndarray:
+    y = _f32(x).copy()
+    lib().jco_relu(_p(y), y.size)
+    return y
+
+
+def add(acc, x) -> np.ndarray:
+    y = _f32(acc).copy()
+    lib().jco_add(_p(y), _p(_f32(x)), y.size)
+    return y
+
+
+def c2_layer(x, w: dict, live, group, rows, n, heads, dh, eps, theta=10000.0, threads=0) -> np.ndarray:
+    """One Chronos-2 encoder layer on x [rows*n, d], in the order CpuChronos2.forward runs it
+    (CpuChronos2.java:150-161): rmsNorm, QKV, RoPE + time attention, O, residual add; the same for
+    group attention; rmsNorm, Wi, ReLU, Wo, residual add. w holds numpy arrays keyed like
+    jc_c2_layer_weights (biases optional)."""
+    inner = heads * dh
+    x = _f32(x)
+    hn = rms_norm(x, w["time_norm"], eps)
+    qkv = linear(hn, w["time_qkv"], w.get("time_qkv_bias"), threads)
+    att = c2_time_attention(qkv, live, rows, n, heads, dh, inner, theta, threads)
+    x = add(x, linear(att, w["time_o"], w.get("time_o_bias"), threads))
+    hn = rms_norm(x, w["group_norm"], eps)
+    qkv = linear(hn, w["group_qkv"], w.get("group_qkv_bias"), threads)
+    att = c2_group_attention(qkv, live, group, rows, n, heads, dh, inner, threads)
+    x = add(x, linear(att, w["group_o"], w.get("group_o_bias"), threads))
+    hn = rms_norm(x, w["mlp_norm"], eps)
+    act = relu(linear(hn, w["wi"], w.get("wi_bias"), threads))
+    return add(x, linear(act, w["wo"], w.get("wo_bias"), threads))
+
+
 def rel_max_error(actual, expected) -> float:
     """The reference's metric: max|a-e| / max(max|e|, 1e-6); a NaN mismatch is infinite
     (T/chronos2/Chronos2Golden.java:218-234)."""

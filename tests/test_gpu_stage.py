@@ -1,0 +1,129 @@
+"""GPU parity of the Chronos-2 encoder layer around the attention cores (through the C ABI):
+jc_linear (Kernels.gemm's flags), jc_rms_norm (Kernels.rmsNorm) and jc_c2_layer (the per-layer stage
+of Chronos2Forward.Plan, Chronos2Forward.java:258-286) against the oracle.
+
+Bar: max relative error (the reference's metric) <= 1e-4 for the fp32 layer; the GEMM and the norm
+alone are held to 1e-5.
+"""
+import numpy as np
+import pytest
+import torch
+
+from jitcast_amd import JitcastArgumentError, chronos2
+from tests import cases
+from tests.test_oracle_ops import _layer_weights
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+TOL = 1e-4
+
+
+def _t(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def _epilogue(y, c0, bias, flags):
+    y = y.astype(np.float64)
+    if bias is not None:
+        y = y + bias.astype(np.float64)
+    if flags & chronos2.GEMM_SILU:
+        y = y / (1 + np.exp(-y))
+    if flags & chronos2.GEMM_RELU:
+        y = np.maximum(y, 0)
+    if flags & chronos2.GEMM_ACCUMULATE:
+        y = y + c0
+    return y
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 16, 16), (37, 100, 64), (129, 130, 784), (300, 257, 48), (256, 128, 128)])
+@pytest.mark.parametrize("flags,bias", [(0, False), (0, True), (chronos2.GEMM_RELU, True),
+                                        (chronos2.GEMM_ACCUMULATE, False), (chronos2.GEMM_ACCUMULATE, True),
+                                        (chronos2.GEMM_SILU, True), (chronos2.GEMM_RELU | chronos2.GEMM_ACCUMULATE, False)])
+def test_linear_matches_oracle(gpu, oracle, m, n, k, flags, bias):
+    print(f"case m={m} n={n} k={k} flags={flags} bias={bias}", flush=True)
+    r = np.random.default_rng(m * 7 + n * 3 + k + flags)
+    a = r.standard_normal((m, k)).astype(np.float32)
+    w = (r.standard_normal((n, k)) / np.sqrt(k)).astype(np.float32)
+    b = r.standard_normal(n).astype(np.float32) if bias else None
+    c0 = r.standard_normal((m, n)).astype(np.float32)
+    c = _t(c0)
+    chronos2.linear(_t(a), _t(w), c, bias=_t(b) if bias else None, flags=flags)
+    torch.cuda.synchronize()
+    exp = _epilogue(oracle.linear(a, w), c0, b, flags)
+    assert oracle.rel_max_error(c.cpu().numpy(), exp) <= 1e-5
+
+
+def test_linear_strided_operands(gpu, oracle):
+    """lda > k (a column slice of a wider activation) and ldc > n (writing into a wider buffer)."""
+    m, n, k, lda, ldc = 70, 48, 32, 40, 64
+    r = np.random.default_rng(3)
+    a_full = r.standard_normal((m, lda)).astype(np.float32)
+    w = r.standard_normal((n, k)).astype(np.float32)
+    c = torch.full((m, ldc), 7.0, device=DEV)
+    chronos2.linear(_t(a_full), _t(w), c, m=m, n=n, k=k, lda=lda, ldc=ldc)
+    torch.cuda.synchronize()
+    got = c.cpu().numpy()
+    assert oracle.rel_max_error(got[:, :n], oracle.linear(np.ascontiguousarray(a_full[:, :k]), w)) <= 1e-5
+    assert (got[:, n:] == 7.0).all()  # columns past n untouched
+
+
+@pytest.mark.parametrize("rows,d", [(1, 4), (13, 64), (300, 768)])
+def test_rms_norm_matches_oracle(gpu, oracle, rows, d):
+    r = np.random.default_rng(rows + d)
+    x = (3 * r.standard_normal((rows, d))).astype(np.float32)
+    w = r.standard_normal(d).astype(np.float32)
+    y = torch.empty(rows, d, device=DEV)
+    chronos2.rms_norm(_t(x), _t(w), y, 1e-6)
+    torch.cuda.synchronize()
+    assert oracle.rel_max_error(y.cpu().numpy(), oracle.rms_norm(x, w, 1e-6)) <= 1e-5
+
+
+def _run_layer(x, w, live, group, rows, n, heads, dh, dff, eps):
+    d = x.shape[1]
+    inner = heads * dh
+    xt = _t(x)
+    wt = {k: _t(v) for k, v in w.items()}
+    gs, ge = chronos2.group_bounds(group)
+    table = _t(chronos2.rope_table(n, dh))
+    nbytes = chronos2.layer_workspace_bytes(rows, n, d, inner, dff)
+    ws = torch.empty(nbytes // 4 + 64, device=DEV)
+    chronos2.layer(xt, wt, _t(live.reshape(-1).astype(np.int32)), table, _t(gs), _t(ge), ws, rows, n, d, heads, dh,
+                   dff, eps)
+    torch.cuda.synchronize()
+    return xt.cpu().numpy()
+
+
+@pytest.mark.parametrize("rows,n,heads,dh,d,dff,bias", [
+    (6, 37, 4, 16, 64, 128, False),
+    (6, 37, 4, 16, 64, 128, True),
+    (4, 37, 8, 64, 512, 2048, False),    # config 0's layer shape (d_model 512, 8 x 64)
+    (3, 130, 12, 64, 768, 3072, False),  # config 4's layer shape (d_model 768, 12 x 64), 130 tokens
+])
+def test_layer_matches_oracle(gpu, oracle, rows, n, heads, dh, d, dff, bias):
+    print(f"case rows={rows} n={n} heads={heads} dh={dh} d={d} dff={dff} bias={bias}", flush=True)
+    w = _layer_weights(21 + d, d, heads * dh, dff, bias)
+    x = np.random.default_rng(22).standard_normal((rows * n, d)).astype(np.float32)
+    live = cases.left_pad_live(23, rows, n, n // 3)
+    group = np.sort(np.random.default_rng(24).integers(0, max(1, rows // 2), rows)).astype(np.int32)
+    got = _run_layer(x, w, live, group, rows, n, heads, dh, dff, 1e-6)
+    exp = oracle.c2_layer(x, w, live, group, rows, n, heads, dh, 1e-6)
+    err = oracle.rel_max_error(got, exp)
+    print(f"  rel err {err:.3e}", flush=True)
+    assert np.isfinite(got).all()
+    assert err <= TOL
+
+
+def test_layer_rejects_bad_arguments(gpu):
+    x = torch.zeros(10, 64, device=DEV)
+    with pytest.raises(JitcastArgumentError):
+        chronos2.linear(x, torch.zeros(8, 60, device=DEV), torch.zeros(10, 8, device=DEV), k=60)  # k % 16
+    with pytest.raises(JitcastArgumentError):
+        chronos2.linear(x, torch.zeros(8, 64, device=DEV), torch.zeros(10, 8, device=DEV),
+                        flags=chronos2.GEMM_RELU | chronos2.GEMM_SILU)
+    with pytest.raises(JitcastArgumentError):
+        chronos2.linear(x, torch.zeros(8, 64, device=DEV), torch.zeros(10, 8, device=DEV), flags=chronos2.GEMM_BIAS)
+    w = {k: torch.zeros(1, device=DEV) for k in ("time_norm", "time_qkv", "time_o", "group_norm", "group_qkv",
+                                                   "group_o", "mlp_norm", "wi", "wo")}
+    ws = torch.zeros(1024, device=DEV)
+    with pytest.raises(JitcastArgumentError):  # dh past 64
+        chronos2.layer(x, w, None, None, None, None, ws, 1, 10, 64, 1, 80, 128, 1e-6)
