@@ -151,6 +151,45 @@ def time_attention_lowp_line(case, steps: int, warmup: int, dtype_name: str) -> 
     return res
 
 
+def layer_line(steps: int, warmup: int) -> dict:
+    """Config 4's encoder-layer shape through jc_c2_layer (fp32): RMSNorm, the six GEMMs of the
+    layer, RoPE time attention, group attention, ReLU and the residual adds."""
+    import torch
+
+    from jitcast_amd import chronos2, synthetic
+
+    case = synthetic.c2_layer_config4(device="cuda")
+    x0 = case.x.clone()
+
+    def fn():
+        chronos2.layer(case.x, case.weights, case.live, case.table, case.group_start, case.group_end, case.workspace,
+                       case.rows, case.n, case.d, case.heads, case.dh, case.dff, 1e-6)
+
+    ms = time_launches(fn, steps, warmup)
+    case.x.copy_(x0)
+    flops = case.flops()
+    tf = flops / (ms * 1e-3) / 1e12
+    tokens = case.rows * case.n
+    log(f"layer: {ms:.3f} ms, {tf:.1f} TFLOP/s ({100 * tf / PEAK_FP32_TFLOPS:.1f}% of the fp32 MFMA peak), "
+        f"{tokens / (ms * 1e-3) / 1e6:.1f} M tokens/s")
+    res = {
+        "workload": "config 4 encoder-layer shape: 1024 groups x (4 series + 1 known covariate), 133 tokens "
+                    "(128 context patches + REG + 4 future), d_model 768, 12x64, d_ff 3072, fp32",
+        "kernel": "jc_c2_layer (jc::gemm_f32 for the GEMMs)",
+        "launch_ms": round(ms, 4),
+        "value": round(tf, 2),
+        "unit": "TFLOP/s",
+        "tokens_per_s": round(tokens / (ms * 1e-3), 1),
+        "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tf / PEAK_FP32_TFLOPS, 4), "traffic": traffic_from_profile("c2_layer_f32_config4")},
+        "flops_per_step": flops,
+        "gemm_share_of_flops": round(case.gemm_flops() / flops, 4),
+    }
+    del case, x0
+    torch.cuda.empty_cache()
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -158,7 +197,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=256)
-    ap.add_argument("--only", choices=["all", "time", "group", "bf16", "fp16"], default="all",
+    ap.add_argument("--only", choices=["all", "time", "group", "bf16", "fp16", "layer"], default="all",
                     help="which workloads to run (profiling runs select one kernel)")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="only run 5 plain device copies of this many bytes (calibrates rocprof byte counters)")
@@ -185,6 +224,11 @@ def main() -> int:
         log(f"copied {args.copy_bytes} bytes 5 times")
         return 0
     also = {}
+    if args.only in ("all", "layer"):
+        also["c2_layer_f32"] = layer_line(max(2, args.steps // 10), 1)
+        if args.only == "layer":
+            print(json.dumps({"also": also}), flush=True)
+            return 0
     if args.only in ("all", "group") and args.only != "time":
         also["c2_group_attention_f32"] = group_attention_line(max(5, args.steps // 2), 2)
         if args.only == "group":

@@ -98,3 +98,65 @@ def c2_group_config2(rows: int = 4096, n: int = 129, heads: int = 12, dh: int = 
     live = torch.ones(rows * n, dtype=torch.int32, device=device)
     return GroupCase(rows, n, heads, dh, inner, qkv, live, torch.from_numpy(s).to(device),
                      torch.from_numpy(e).to(device), group)
+
+
+@dataclass
+class LayerCase:
+    rows: int
+    n: int
+    heads: int
+    dh: int
+    d: int
+    dff: int
+    groups: int
+    x: object  # torch [rows*n, d]
+    weights: dict  # torch tensors keyed like jc_c2_layer_weights
+    live: object  # torch int32 [rows*n]
+    table: object  # torch float32 [n, dh]
+    group_start: object  # torch int32 [rows]
+    group_end: object
+    workspace: object  # torch float32, jc_c2_layer_workspace_bytes
+
+    def gemm_flops(self) -> float:
+        t, d, inner = self.rows * self.n, self.d, self.heads * self.dh
+        return 2.0 * t * d * (2 * 3 * inner + 2 * inner + 2 * self.dff)
+
+    def attention_flops(self) -> float:
+        """time attention over every (live) key of the row, group attention over the group's rows."""
+        per_group = self.rows // self.groups
+        live = float(self.live.double().sum().item())
+        return 4.0 * self.dh * self.heads * (self.n * live + per_group * live)
+
+    def flops(self) -> float:
+        return self.gemm_flops() + self.attention_flops()
+
+
+def c2_layer_config4(groups: int = 1024, per_group: int = 5, nc: int = 128, h: int = 4, heads: int = 12, dh: int = 64,
+                     d: int = 768, dff: int = 3072, seed: int = 0, device: str = "cuda") -> LayerCase:
+    """Config 4's encoder-layer shape: 1024 groups of 4 target series plus their known-future covariate
+    (5 rows each), 2048-step contexts fully observed (128 patches) + [REG] + 4 future patches = 133
+    tokens; Chronos-2 120M-class layer (d_model 768, 12 x 64, d_ff 3072), weights N(0, 0.02), norm
+    weights 1, activations x ~ N(0, 1)."""
+    import torch
+
+    from .chronos2 import layer_workspace_bytes
+
+    rows, n, inner = groups * per_group, nc + 1 + h, heads * dh
+    x = torch.empty(rows * n, d, dtype=torch.float32, device=device)
+    fill_normal(x, rng.stream_seed(seed, 10), 0.0, 1.0)
+    shapes = {"time_qkv": (3 * inner, d), "time_o": (d, inner), "group_qkv": (3 * inner, d), "group_o": (d, inner),
+              "wi": (dff, d), "wo": (d, dff)}
+    weights = {}
+    for i, (name, shape) in enumerate(shapes.items()):
+        t = torch.empty(shape, dtype=torch.float32, device=device)
+        fill_normal(t, rng.stream_seed(seed, 11 + i), 0.0, 0.02)
+        weights[name] = t
+    for name in ("time_norm", "group_norm", "mlp_norm"):
+        weights[name] = torch.ones(d, dtype=torch.float32, device=device)
+    live = torch.ones(rows * n, dtype=torch.int32, device=device)
+    starts = (np.arange(rows) // per_group * per_group).astype(np.int32)
+    gs = torch.from_numpy(starts).to(device)
+    ge = torch.from_numpy(starts + per_group).to(device)
+    table = torch.from_numpy(rope_table(n, dh)).to(device)
+    ws = torch.empty(layer_workspace_bytes(rows, n, d, inner, dff) // 4 + 64, dtype=torch.float32, device=device)
+    return LayerCase(rows, n, heads, dh, d, dff, groups, x, weights, live, table, gs, ge, ws)
