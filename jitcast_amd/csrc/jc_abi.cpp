@@ -62,11 +62,12 @@ int use(jc_ctx* ctx, const char* where) {
 
 size_t dtype_size(int dtype) { return dtype == JC_F32 ? 4 : 2; }
 
-// JITCAST_HIP_LPW=1 sends bf16/fp16 rows that fit it to the row-wide kernel (read at every launch, so
-// a host can switch between the kernels at run time)
-bool lpw_enabled() {
-    const char* e = getenv("JITCAST_HIP_LPW");
-    return e && e[0] == '1';
+// JITCAST_HIP_LP_KERNEL picks the bf16/fp16 time-attention kernel: "wide" (time_attention_lpw, the
+// default, for the shapes it takes) or "stream" (time_attention_lp, which takes every shape). Read at
+// every launch, so a host can switch at run time.
+bool lp_stream_only() {
+    const char* e = getenv("JITCAST_HIP_LP_KERNEL");
+    return e && !strcmp(e, "stream");
 }
 
 }  // namespace
@@ -273,17 +274,18 @@ static int check_time_common(const char* W, const void* qkv, const void* out, co
     return JC_OK;
 }
 
-// fp32 goes to the fp32 kernel; bf16/fp16 to the streaming kernel, or to the row-wide one when asked
-// for and the shape fits it (both give the same results to within rounding; neither is faster on
-// every shape).
+// fp32 goes to the fp32 kernel; bf16/fp16 to the row-wide kernel when the shape fits it (unless
+// JITCAST_HIP_LP_KERNEL=stream), else to the streaming kernel, which takes every shape. Both give
+// the same results to within rounding.
 static int launch_time(jc_ctx* ctx, const char* W, const jc::TimeArgs& a, int dh, bool ts, int dtype) {
     hipError_t e;
+    const bool fp16 = dtype == JC_F16;
     if (dtype == JC_F32) {
         e = jc::time_attention_f32_launch(a, dh, ts, ctx->stream);
-    } else if (lpw_enabled() && jc::time_attention_lpw_fits(a, dh)) {
-        e = jc::time_attention_lpw_launch(a, dh, ts, dtype == JC_F16, ctx->stream);
+    } else if (!lp_stream_only() && jc::time_attention_lpw_fits(a, dh)) {
+        e = jc::time_attention_lpw_launch(a, dh, ts, fp16, ctx->stream);
     } else {
-        e = jc::time_attention_lp_launch(a, dh, ts, dtype == JC_F16, ctx->stream);
+        e = jc::time_attention_lp_launch(a, dh, ts, fp16, ctx->stream);
     }
     return e == hipSuccess ? JC_OK : hip_fail(W, e);
 }

@@ -14,7 +14,9 @@
 //     RoPE pair and exchange them with v_permlane32_swap. The rotation's cos/sin for position p are
 //     composed in fp32 from two LDS tables taken from rows of the host table: T_lo (positions
 //     0..63) and T_hi (positions 64a), cos(p f) = cos(64a f) cos(b f) - sin(64a f) sin(b f) for
-//     p = 64a + b, so no table rows stream per block.
+//     p = 64a + b, so no table rows stream per block. Table rows are padded to DH+4 floats: the 8
+//     lanes of one 128-byte LDS cycle read 8 consecutive positions, which then fall on distinct
+//     banks (at a 256-byte pitch every row starts on the same bank: an 8-way conflict).
 //   V item (4 keys, 2 dims): four 4-byte loads written as two 8-byte rows of V^T, keys permuted
 //     within 16-key groups as in time_attention_lp.hip.
 // Each wave computes its tile in 32-key sub-blocks (S^T 16 VGPRs, P 8), which keeps the kernel
@@ -45,8 +47,9 @@ struct WideLds {
     static constexpr int kPitchV = kKB + 8;  // elements per dim row of V^T
     uint16_t k[2][kKB * kPitchK];
     uint16_t vt[2][DH * kPitchV];
-    float tlo[kKB * DH];     // cos | sin of b * invFreq, b < 64
-    float thi[kMaxHi * DH];  // cos | sin of the angle of table row 64a
+    static constexpr int kPitchT = DH + 4;  // floats per table row (rows of consecutive positions on distinct banks)
+    float tlo[kKB * kPitchT];     // cos | sin of b * invFreq, b < 64
+    float thi[kMaxHi * kPitchT];  // cos | sin of the angle of table row 64a
     uint64_t mask[kMaxTokens / kKB];
     int32_t pos[TS ? kMaxTokens : 1];
 };
@@ -98,6 +101,7 @@ struct WideStage {
     template <int SET>
     __device__ __forceinline__ void store(WideLds<DH, TS>& lds, int buf, int kbase, int n) {
         constexpr int PK = WideLds<DH, TS>::kPitchK, PV = WideLds<DH, TS>::kPitchV;
+        constexpr int PT = WideLds<DH, TS>::kPitchT;
         if (has_k) {
             u32x4 w = kraw[SET];
             if (ROPE) {
@@ -113,8 +117,8 @@ struct WideStage {
                 widen8<T>(part, y0, y1);
                 const int k = kbase + kk;
                 const int p = TS ? (k < n ? lds.pos[k] : 0) : k;
-                const float* hi = &lds.thi[(p >> 6) * DH + tcol];
-                const float* lo = &lds.tlo[(p & 63) * DH + tcol];
+                const float* hi = &lds.thi[(p >> 6) * PT + tcol];
+                const float* lo = &lds.tlo[(p & 63) * PT + tcol];
                 floatx4 r[2];
 #pragma unroll
                 for (int q = 0; q < 2; q++) {
@@ -151,6 +155,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     constexpr int kSteps = DH / 16;  // QK^T MFMA steps (16 dims each), plus the bias step
     constexpr int kTiles = DH / 32;  // 32-dim output tiles
     constexpr int PK = WideLds<DH, TS>::kPitchK, PV = WideLds<DH, TS>::kPitchV;
+    constexpr int PT = WideLds<DH, TS>::kPitchT;
     typedef typename Lp<T>::x8 x8;
     typedef Enc<T> E;
     __shared__ WideLds<DH, TS> lds;
@@ -208,12 +213,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
 #pragma unroll
         for (int i = 0; i < kLoPer; i++) {
             const int f = tid + i * kThreads;
-            if (f < kLo) reinterpret_cast<floatx4*>(lds.tlo)[f] = lo4[i];
+            if (f < kLo) *reinterpret_cast<floatx4*>(&lds.tlo[(f / (DH / 4)) * PT + 4 * (f % (DH / 4))]) = lo4[i];
         }
 #pragma unroll
         for (int i = 0; i < kHiPer; i++) {
             const int f = tid + i * kThreads;
-            if (f < nhi4) reinterpret_cast<floatx4*>(lds.thi)[f] = hi4[i];
+            if (f < nhi4) *reinterpret_cast<floatx4*>(&lds.thi[(f / (DH / 4)) * PT + 4 * (f % (DH / 4))]) = hi4[i];
         }
     }
     const int nblk = (n + kKB - 1) / kKB;
@@ -248,8 +253,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
                     const int e0 = first ? d0 : d0 - half;
                     floatx4 plo, phi;
                     widen8<T>(q_par[s], plo, phi);
-                    const float* th = &lds.thi[(p >> 6) * DH + e0];
-                    const float* tl = &lds.tlo[(p & 63) * DH + e0];
+                    const float* th = &lds.thi[(p >> 6) * PT + e0];
+                    const float* tl = &lds.tlo[(p & 63) * PT + e0];
 #pragma unroll
                     for (int part = 0; part < 2; part++) {
                         const floatx4 ch = *reinterpret_cast<const floatx4*>(th + 4 * part);

@@ -43,15 +43,11 @@ def gpu():
 
 @pytest.fixture(params=["stream", "wide"])
 def lp_kernel(request, monkeypatch):
-    """Which bf16/fp16 time-attention kernel the library launches: the streaming one (default) or the
-    row-wide one (JITCAST_HIP_LPW=1; used for rows of 256+ tokens with head width 32 or 64)."""
-    monkeypatch.setenv("JITCAST_HIP_LPW", "1" if request.param == "wide" else "0")
+    """Which bf16/fp16 time-attention kernel the library launches (JITCAST_HIP_LP_KERNEL): the
+    streaming one, or the row-wide one (the default, for rows of 256+ tokens and head width 32 or
+    64; other shapes fall back to the streaming kernel)."""
+    monkeypatch.setenv("JITCAST_HIP_LP_KERNEL", request.param)
     return request.param
-
-
-def wide_fits(n, dh):
-    """Whether the row-wide kernel takes this shape (else both settings run the streaming kernel)."""
-    return n >= 256 and dh in (32, 64)
 
 
 @pytest.fixture(scope="session", autouse=True)

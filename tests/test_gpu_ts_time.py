@@ -10,7 +10,6 @@ import torch
 
 from jitcast_amd import JitcastArgumentError, timestral
 from tests import cases
-from tests.conftest import wide_fits
 
 pytestmark = pytest.mark.gpu
 TOL_F32 = 1e-4
@@ -79,8 +78,7 @@ def test_fp32_matches_oracle(gpu, oracle, rows, enc, ll, h, heads, dh, d, rope_d
 @pytest.mark.parametrize("dt", ["bf16", "fp16"])
 @pytest.mark.parametrize("rows,enc,ll,h,heads,dh,d,rope_dim,known_frac,gate", [c for c in CASES if c[5] % 16 == 0])
 def test_lowp_matches_oracle(gpu, oracle, rows, enc, ll, h, heads, dh, d, rope_dim, known_frac, gate, dt, lp_kernel):
-    if lp_kernel == "wide" and not wide_fits(enc + h, dh):
-        pytest.skip("the row-wide kernel does not take this shape")
+    # (a shape the chosen kernel does not take runs on the streaming kernel: the fallback is tested too)
     print(f"case {dt} {lp_kernel} rows={rows} enc={enc} ll={ll} h={h} heads={heads} dh={dh} known={known_frac} gate={gate}",
           flush=True)
     n, qkv, kv, known, position, g = _inputs(89, rows, enc, ll, h, d, known_frac, gate)
@@ -102,11 +100,12 @@ def test_fp32_without_table_is_plain_masked_attention(gpu, oracle):
     assert oracle.rel_max_error(got[:, : heads * dh], exp[:, : heads * dh]) <= TOL_F32
 
 
-@pytest.mark.parametrize("dt", ["fp32", "bf16", "bf16-wide"])
+@pytest.mark.parametrize("dt", ["fp32", "bf16-stream", "bf16-wide"])
 def test_config3_shape_subset(gpu, oracle, dt, monkeypatch):
     """Config 3's attention shape (1024 tokens, 12x64, rope_partial_factor 0.5, gate on, every row
     known = bidirectional, left padding U{0..256}) on 2 series."""
-    monkeypatch.setenv("JITCAST_HIP_LPW", "1" if dt == "bf16-wide" else "0")
+    if "-" in dt:
+        monkeypatch.setenv("JITCAST_HIP_LP_KERNEL", dt.split("-")[1])
     dt = dt.split("-")[0]
     rows, enc, heads, dh, d, rope_dim = 2, 1024, 12, 64, 768, 32
     qkv = cases.qkv(101, rows * enc, d, std=0.6)
