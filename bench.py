@@ -190,6 +190,42 @@ def layer_line(steps: int, warmup: int) -> dict:
     return res
 
 
+def ts_time_attention_line(steps: int, warmup: int) -> dict:
+    """Config 3's attention stack: the bf16 Timestral time attention (RoPE, mask, fused gate) of 12
+    layers per step on 64 series x 1024 tokens, 12 x 64 heads."""
+    import torch
+
+    from jitcast_amd import synthetic, timestral
+
+    case = synthetic.ts_time_config3(device="cuda")
+    out = torch.empty(case.rows * case.n, case.d, dtype=torch.bfloat16, device="cuda")
+    layers = 12
+
+    def fn():
+        for _ in range(layers):
+            timestral.time_attention(case.qkv, out, case.key_valid, case.known, case.pos, case.table, case.gate,
+                                     case.rows, case.n, case.n, case.n, case.heads, case.dh, case.d)
+
+    ms = time_launches(fn, steps, warmup)
+    flops = layers * case.mask_aware_flops()
+    tf = flops / (ms * 1e-3) / 1e12
+    log(f"config 3 attention stack bf16: {ms:.3f} ms for {layers} layers, {tf:.1f} TFLOP/s mask-aware "
+        f"({100 * tf / PEAK_BF16_TFLOPS:.1f}% of the bf16 MFMA peak)")
+    res = {
+        "workload": "config 3: Timestral time attention in bf16 (RoPE on half the head, bidirectional over valid "
+                    "keys, left padding U{0..256}, fused gate), 64 series x 1024 tokens, 12x64, 12 layers per step",
+        "kernel": "jc::time_attention_lpw<__bf16, 64, true, true>",
+        "launch_ms": round(ms / layers, 5),
+        "value": round(tf, 2),
+        "unit": "TFLOP/s",
+        "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tf / PEAK_BF16_TFLOPS, 4), "traffic": None},
+    }
+    del case, out
+    torch.cuda.empty_cache()
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -197,7 +233,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=256)
-    ap.add_argument("--only", choices=["all", "time", "group", "bf16", "fp16", "layer"], default="all",
+    ap.add_argument("--only", choices=["all", "time", "group", "bf16", "fp16", "layer", "ts"], default="all",
                     help="which workloads to run (profiling runs select one kernel)")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="only run 5 plain device copies of this many bytes (calibrates rocprof byte counters)")
@@ -224,6 +260,11 @@ def main() -> int:
         log(f"copied {args.copy_bytes} bytes 5 times")
         return 0
     also = {}
+    if args.only in ("all", "ts"):
+        also["ts_time_attention_bf16"] = ts_time_attention_line(max(3, args.steps // 5), 1)
+        if args.only == "ts":
+            print(json.dumps({"also": also}), flush=True)
+            return 0
     if args.only in ("all", "layer"):
         also["c2_layer_f32"] = layer_line(max(2, args.steps // 10), 1)
         if args.only == "layer":

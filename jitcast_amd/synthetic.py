@@ -160,3 +160,55 @@ def c2_layer_config4(groups: int = 1024, per_group: int = 5, nc: int = 128, h: i
     table = torch.from_numpy(rope_table(n, dh)).to(device)
     ws = torch.empty(layer_workspace_bytes(rows, n, d, inner, dff) // 4 + 64, dtype=torch.float32, device=device)
     return LayerCase(rows, n, heads, dh, d, dff, groups, x, weights, live, table, gs, ge, ws)
+
+
+@dataclass
+class TsTimeCase:
+    rows: int
+    n: int
+    heads: int
+    dh: int
+    d: int
+    qkv: object  # torch bf16 [rows*n, 3*d]
+    gate: object  # torch bf16 [rows*n, d]
+    key_valid: object  # torch int32 [rows*n]
+    known: object  # torch int32 [rows]
+    pos: object  # torch int32 [rows*n]: table rows (position + n)
+    table: object  # torch float32 [2n, dh]
+    starts: np.ndarray
+
+    def mask_aware_flops(self) -> float:
+        """4*dh per (row, head, query, allowed key): every valid key (k >= start, known rows read
+        both directions) plus the query itself where it is not a valid key."""
+        per_row = [(self.n - s) * self.n + s for s in self.starts]
+        return 4.0 * self.dh * self.heads * float(sum(per_row))
+
+
+def ts_time_config3(rows: int = 64, n: int = 1024, heads: int = 12, dh: int = 64, d: int = 768, rope_dim: int = 32,
+                    max_start: int = 256, seed: int = 0, device: str = "cuda") -> TsTimeCase:
+    """Config 3's time-attention sublayer: Timestral 123M-class (d_model 768, 12 x 64,
+    rope_partial_factor 0.5), 64 series x 1024 patch tokens, x ~ N(0, 1), projections N(0, 0.02),
+    q|k|v and the gate projection in bf16; bidirectional (every row a known covariate, so each
+    query reads every valid key) with left padding U{0..256} masked (attend_missing_patches: keys
+    from the first observed patch on are valid); positions count from the first observed patch."""
+    import torch
+
+    from .timestral import rope_table as ts_rope_table
+
+    x = torch.empty(rows * n, d, dtype=torch.float32, device=device)
+    w = torch.empty(4 * d, d, dtype=torch.float32, device=device)
+    fill_normal(x, rng.stream_seed(seed, 20), 0.0, 1.0)
+    fill_normal(w, rng.stream_seed(seed, 21), 0.0, 0.02)
+    proj = (x @ w.t()).to(torch.bfloat16)
+    del x, w
+    qkv = proj[:, : 3 * d].contiguous()
+    gate = proj[:, 3 * d:].contiguous()
+    del proj
+    starts = rng.randint(rng.stream_seed(seed, 22), rows, 0, max_start)
+    t = np.arange(n)[None, :]
+    key_valid = (t >= starts[:, None]).astype(np.int32)
+    pos = (t - starts[:, None] + n).astype(np.int32)  # table row = position + enc
+    known = np.ones(rows, np.int32)
+    table = torch.from_numpy(ts_rope_table(n, n, dh, rope_dim)).to(device)
+    return TsTimeCase(rows, n, heads, dh, d, qkv, gate, torch.from_numpy(key_valid.reshape(-1)).to(device),
+                      torch.from_numpy(known).to(device), torch.from_numpy(pos.reshape(-1)).to(device), table, starts)
