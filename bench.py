@@ -214,7 +214,7 @@ def ts_time_attention_line(steps: int, warmup: int) -> dict:
     res = {
         "workload": "config 3: Timestral time attention in bf16 (RoPE on half the head, bidirectional over valid "
                     "keys, left padding U{0..256}, fused gate), 64 series x 1024 tokens, 12x64, 12 layers per step",
-        "kernel": "jc::time_attention_lpw<__bf16, 64, true, true>",
+        "kernel": "jc::time_attention_lp<__bf16, 64, 4, true, true, true>",
         "launch_ms": round(ms / layers, 5),
         "value": round(tf, 2),
         "unit": "TFLOP/s",

@@ -62,12 +62,16 @@ int use(jc_ctx* ctx, const char* where) {
 
 size_t dtype_size(int dtype) { return dtype == JC_F32 ? 4 : 2; }
 
-// JITCAST_HIP_LP_KERNEL picks the bf16/fp16 time-attention kernel: "wide" (time_attention_lpw, the
-// default, for the shapes it takes) or "stream" (time_attention_lp, which takes every shape). Read at
-// every launch, so a host can switch at run time.
-bool lp_stream_only() {
+// JITCAST_HIP_LP_KERNEL picks the bf16/fp16 time-attention kernel: "stream" (time_attention_lp,
+// which takes every shape) or "wide" (time_attention_lpw, for the shapes it takes). Unset, Chronos-2
+// uses the row-wide kernel and Timestral the streaming one: its row-wide variant holds every
+// token's table row in LDS and fits one workgroup per CU (measured on config 3: 6.30 ms against
+// 6.04 ms per 12 layers). Read at every launch, so a host can switch at run time.
+bool lp_use_wide(bool ts) {
     const char* e = getenv("JITCAST_HIP_LP_KERNEL");
-    return e && !strcmp(e, "stream");
+    if (e && !strcmp(e, "stream")) return false;
+    if (e && !strcmp(e, "wide")) return true;
+    return !ts;
 }
 
 }  // namespace
@@ -274,15 +278,15 @@ static int check_time_common(const char* W, const void* qkv, const void* out, co
     return JC_OK;
 }
 
-// fp32 goes to the fp32 kernel; bf16/fp16 to the row-wide kernel when the shape fits it (unless
-// JITCAST_HIP_LP_KERNEL=stream), else to the streaming kernel, which takes every shape. Both give
-// the same results to within rounding.
+// fp32 goes to the fp32 kernel; bf16/fp16 to the row-wide kernel when lp_use_wide() picks it and
+// the shape fits it, else to the streaming kernel, which takes every shape. Both give the same
+// results to within rounding.
 static int launch_time(jc_ctx* ctx, const char* W, const jc::TimeArgs& a, int dh, bool ts, int dtype) {
     hipError_t e;
     const bool fp16 = dtype == JC_F16;
     if (dtype == JC_F32) {
         e = jc::time_attention_f32_launch(a, dh, ts, ctx->stream);
-    } else if (!lp_stream_only() && jc::time_attention_lpw_fits(a, dh)) {
+    } else if (lp_use_wide(ts) && jc::time_attention_lpw_fits(a, dh)) {
         e = jc::time_attention_lpw_launch(a, dh, ts, fp16, ctx->stream);
     } else {
         e = jc::time_attention_lp_launch(a, dh, ts, fp16, ctx->stream);

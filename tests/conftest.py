@@ -44,8 +44,9 @@ def gpu():
 @pytest.fixture(params=["stream", "wide"])
 def lp_kernel(request, monkeypatch):
     """Which bf16/fp16 time-attention kernel the library launches (JITCAST_HIP_LP_KERNEL): the
-    streaming one, or the row-wide one (the default, for rows of 256+ tokens and head width 32 or
-    64; other shapes fall back to the streaming kernel)."""
+    streaming one, or the row-wide one (rows of 256+ tokens and head width 32 or 64; other shapes
+    fall back to the streaming kernel). Unset, Chronos-2 uses the row-wide kernel, Timestral the
+    streaming one."""
     monkeypatch.setenv("JITCAST_HIP_LP_KERNEL", request.param)
     return request.param
 
