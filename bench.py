@@ -151,41 +151,56 @@ def time_attention_lowp_line(case, steps: int, warmup: int, dtype_name: str) -> 
     return res
 
 
-def layer_line(steps: int, warmup: int) -> dict:
-    """Config 4's encoder-layer shape through jc_c2_layer (fp32): RMSNorm, the six GEMMs of the
-    layer, RoPE time attention, group attention, ReLU and the residual adds."""
+def layer_line(steps: int, warmup: int, dtype_name: str = "f32") -> dict:
+    """Config 4's encoder-layer shape through jc_c2_layer: RMSNorm, the six GEMMs of the layer, RoPE
+    time attention, group attention, ReLU and the residual adds. f32: everything fp32. bf16: the
+    GEMMs and the time attention in bf16 with fp32 accumulation (weights converted once, outside the
+    timed region), the group attention, norms and residual stream fp32."""
     import torch
 
-    from jitcast_amd import chronos2, synthetic
+    from jitcast_amd import _lib, chronos2, synthetic
 
     case = synthetic.c2_layer_config4(device="cuda")
+    code = {"f32": _lib.JC_F32, "bf16": _lib.JC_BF16}[dtype_name]
+    weights = dict(case.weights)
+    ws = case.workspace
+    if code != _lib.JC_F32:
+        for k in ("time_qkv", "time_o", "group_qkv", "group_o", "wi", "wo"):
+            lp = torch.empty(weights[k].shape, dtype=torch.bfloat16, device="cuda")
+            chronos2.to_lp(weights[k], lp)
+            weights[k] = lp
+        inner = case.heads * case.dh
+        ws = torch.empty(chronos2.layer_workspace_bytes(case.rows, case.n, case.d, inner, case.dff, code) // 4 + 64,
+                         dtype=torch.float32, device="cuda")
     x0 = case.x.clone()
 
     def fn():
-        chronos2.layer(case.x, case.weights, case.live, case.table, case.group_start, case.group_end, case.workspace,
-                       case.rows, case.n, case.d, case.heads, case.dh, case.dff, 1e-6)
+        chronos2.layer(case.x, weights, case.live, case.table, case.group_start, case.group_end, ws, case.rows,
+                       case.n, case.d, case.heads, case.dh, case.dff, 1e-6, code)
 
     ms = time_launches(fn, steps, warmup)
     case.x.copy_(x0)
     flops = case.flops()
     tf = flops / (ms * 1e-3) / 1e12
+    peak = PEAK_FP32_TFLOPS if code == _lib.JC_F32 else PEAK_BF16_TFLOPS
     tokens = case.rows * case.n
-    log(f"layer: {ms:.3f} ms, {tf:.1f} TFLOP/s ({100 * tf / PEAK_FP32_TFLOPS:.1f}% of the fp32 MFMA peak), "
+    log(f"layer {dtype_name}: {ms:.3f} ms, {tf:.1f} TFLOP/s ({100 * tf / peak:.1f}% of the {dtype_name} MFMA peak), "
         f"{tokens / (ms * 1e-3) / 1e6:.1f} M tokens/s")
     res = {
-        "workload": "config 4 encoder-layer shape: 1024 groups x (4 series + 1 known covariate), 133 tokens "
-                    "(128 context patches + REG + 4 future), d_model 768, 12x64, d_ff 3072, fp32",
-        "kernel": "jc_c2_layer (jc::gemm_f32 for the GEMMs)",
+        "workload": f"config 4 encoder-layer shape: 1024 groups x (4 series + 1 known covariate), 133 tokens "
+                    f"(128 context patches + REG + 4 future), d_model 768, 12x64, d_ff 3072, {dtype_name}",
+        "kernel": "jc_c2_layer (%s for the GEMMs)" % ("jc::gemm_f32" if code == _lib.JC_F32 else "jc::gemm_lp<__bf16>"),
         "launch_ms": round(ms, 4),
         "value": round(tf, 2),
         "unit": "TFLOP/s",
         "tokens_per_s": round(tokens / (ms * 1e-3), 1),
-        "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(tf / PEAK_FP32_TFLOPS, 4), "traffic": traffic_from_profile("c2_layer_f32_config4")},
+        "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": peak, "unit": "TFLOP/s",
+                     "frac": round(tf / peak, 4),
+                     "traffic": traffic_from_profile(f"c2_layer_{dtype_name}_config4")},
         "flops_per_step": flops,
         "gemm_share_of_flops": round(case.gemm_flops() / flops, 4),
     }
-    del case, x0
+    del case, x0, weights, ws
     torch.cuda.empty_cache()
     return res
 
@@ -233,7 +248,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=256)
-    ap.add_argument("--only", choices=["all", "time", "group", "bf16", "fp16", "layer", "ts"], default="all",
+    ap.add_argument("--only", choices=["all", "time", "group", "bf16", "fp16", "layer", "layer-bf16", "ts"], default="all",
                     help="which workloads to run (profiling runs select one kernel)")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="only run 5 plain device copies of this many bytes (calibrates rocprof byte counters)")
@@ -263,6 +278,11 @@ def main() -> int:
     if args.only in ("all", "ts"):
         also["ts_time_attention_bf16"] = ts_time_attention_line(max(3, args.steps // 5), 1)
         if args.only == "ts":
+            print(json.dumps({"also": also}), flush=True)
+            return 0
+    if args.only in ("all", "layer-bf16"):
+        also["c2_layer_bf16"] = layer_line(max(3, args.steps // 5), 1, "bf16")
+        if args.only == "layer-bf16":
             print(json.dumps({"also": also}), flush=True)
             return 0
     if args.only in ("all", "layer"):

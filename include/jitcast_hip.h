@@ -286,31 +286,34 @@ int jc_linear(jc_ctx *ctx, const float *a, int lda, const float *w, const float 
 int jc_rms_norm(jc_ctx *ctx, const float *x, const float *w, float *y, int rows, int d, float eps);
 
 /* Device weights of one Chronos-2 encoder layer (Chronos2Packed.Layer, Chronos2Packed.java:41-47,
- * 150-154); a bias pointer may be NULL (no bias). */
+ * 150-154). The matrices are fp32 for a JC_F32 layer and bf16 / fp16 for a JC_BF16 / JC_F16 layer
+ * (jc_to_lp converts them once); norm weights and biases are always fp32. A bias may be NULL. */
 typedef struct jc_c2_layer_weights {
     const float *time_norm;  /* [d] */
-    const float *time_qkv;   /* [3*inner, d]: q | k | v rows, heads-major */
+    const void *time_qkv;    /* [3*inner, d]: q | k | v rows, heads-major */
     const float *time_qkv_bias;
-    const float *time_o;     /* [d, inner] */
+    const void *time_o;      /* [d, inner] */
     const float *time_o_bias;
     const float *group_norm; /* [d] */
-    const float *group_qkv;  /* [3*inner, d] */
+    const void *group_qkv;   /* [3*inner, d] */
     const float *group_qkv_bias;
-    const float *group_o;    /* [d, inner] */
+    const void *group_o;     /* [d, inner] */
     const float *group_o_bias;
     const float *mlp_norm;   /* [d] */
-    const float *wi;         /* [dff, d] */
+    const void *wi;          /* [dff, d] */
     const float *wi_bias;
-    const float *wo;         /* [d, dff] */
+    const void *wo;          /* [d, dff] */
     const float *wo_bias;
 } jc_c2_layer_weights;
 
-/* Bytes of the workspace jc_c2_layer needs (hn [T, d], big [T, max(3*inner, dff)], att [T, inner]
- * floats for T = rows*n tokens, each part 256-byte aligned), or -1 for a negative size. */
-int64_t jc_c2_layer_workspace_bytes(int rows, int n, int d, int inner, int dff);
+/* Bytes of the workspace jc_c2_layer needs for T = rows*n tokens, each part 256-byte aligned, or
+ * -1 for a negative size. JC_F32: hn [T, d], big [T, max(3*inner, dff)], att [T, inner] floats.
+ * JC_BF16 / JC_F16: hn [T, d] and att [T, inner] in the storage type, big [T, max(3*inner floats,
+ * dff storage values)] and an fp32 att [T, inner] for the group attention. */
+int64_t jc_c2_layer_workspace_bytes(int rows, int n, int d, int inner, int dff, int dtype);
 
 /*
- * One Chronos-2 encoder layer in place on x [rows*n, d] (the per-layer stage of
+ * One Chronos-2 encoder layer in place on x [rows*n, d] fp32 (the per-layer stage of
  * Chronos2Forward.Plan, J/chronos2/tornado/Chronos2Forward.java:258-286; CPU CpuChronos2.forward,
  * J/chronos2/cpu/CpuChronos2.java:150-161):
  *   x += O_time(timeAttention(RoPE(QKV_time(rmsNorm(x)))))
@@ -320,10 +323,33 @@ int64_t jc_c2_layer_workspace_bytes(int rows, int n, int d, int inner, int dff);
  * jc_c2_time_attention and jc_c2_group_attention (groups contiguous); workspace of
  * jc_c2_layer_workspace_bytes, 256-byte aligned. inner = heads*dh. d a multiple of 16, dh a multiple
  * of 16 and at most 64, dff a multiple of 16.
+ * dtype JC_F32: everything in fp32. JC_BF16 / JC_F16: the GEMMs take the storage type with fp32
+ * accumulation (the reference's FP16 GEMM modes, Chronos2Forward.java:377-409, GemmMode.HALF), the
+ * time attention runs in the storage type, the group attention in fp32, and x (the residual
+ * stream), the norms and the accumulations stay fp32.
  */
 int jc_c2_layer(jc_ctx *ctx, float *x, const jc_c2_layer_weights *w, const int32_t *live, const float *table,
                 const int32_t *group_start, const int32_t *group_end, void *workspace, int rows, int n, int d,
-                int heads, int dh, int dff, float eps);
+                int heads, int dh, int dff, float eps, int dtype);
+
+/*
+ * bf16 / fp16 GEMM with fp32 accumulation: C[m, n] (+)= act(A[m, :k] . W[n, :k] + bias[n]), A and W
+ * in the storage type `dtype` (JC_BF16 or JC_F16), bias fp32. c_dtype JC_F32: C fp32, any flags
+ * (JC_GEMM_ACCUMULATE adds into C). c_dtype = dtype: C in the storage type, saturated to its finite
+ * range (the reference's FP16 twins, Kernels.java:42-46), no ACCUMULATE. Replaces Kernels.gemmHalf
+ * and the GemmEx FP16->FP32 path (J/tornado/Kernels.java:115-232; Chronos2Forward.java:377-409).
+ *   k a multiple of 8, lda >= k and a multiple of 8, ldc >= n; a and w 16-byte aligned.
+ */
+int jc_linear_lp(jc_ctx *ctx, const void *a, int lda, const void *w, const float *bias, void *c, int ldc, int m,
+                 int n, int k, int flags, int dtype, int c_dtype);
+
+/* Kernels.rmsNorm with its twin output (J/tornado/Kernels.java:800-829): y in the storage type
+ * `dtype` = x * (1 / sqrt(mean(x^2) + eps)) * w, x fp32; d a multiple of 4; 16-byte aligned. */
+int jc_rms_norm_lp(jc_ctx *ctx, const float *x, const float *w, void *y, int rows, int d, float eps, int dtype);
+
+/* dst[i] = src[i] rounded to the storage type `dtype`, saturated to its finite range (Kernels.toHalf,
+ * J/tornado/Kernels.java:887-895): for weights, converted once. */
+int jc_to_lp(jc_ctx *ctx, const float *src, void *dst, int64_t count, int dtype);
 
 #ifdef __cplusplus
 }

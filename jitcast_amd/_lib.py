@@ -74,8 +74,11 @@ SIGNATURES = {
     "jc_c2_group_bounds": (_i, [_vp, _i, _vp, _vp]),
     "jc_linear": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _i]),
     "jc_rms_norm": (_i, [_vp, _vp, _vp, _vp, _i, _i, _f]),
-    "jc_c2_layer_workspace_bytes": (_c.c_int64, [_i, _i, _i, _i, _i]),
-    "jc_c2_layer": (_i, [_vp, _vp, _vp, _i32p, _vp, _i32p, _i32p, _vp, _i, _i, _i, _i, _i, _i, _f]),
+    "jc_c2_layer_workspace_bytes": (_c.c_int64, [_i, _i, _i, _i, _i, _i]),
+    "jc_c2_layer": (_i, [_vp, _vp, _vp, _i32p, _vp, _i32p, _i32p, _vp, _i, _i, _i, _i, _i, _i, _f, _i]),
+    "jc_linear_lp": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i]),
+    "jc_rms_norm_lp": (_i, [_vp, _vp, _vp, _vp, _i, _i, _f, _i]),
+    "jc_to_lp": (_i, [_vp, _vp, _vp, _c.c_int64, _i]),
     "jc_ts_block_layout": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _c.POINTER(_i), _c.POINTER(_i), _vp,
                                 _vp, _vp]),
 }

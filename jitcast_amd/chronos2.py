@@ -154,15 +154,51 @@ class LayerWeights(ctypes.Structure):
         return lw
 
 
-def layer_workspace_bytes(rows: int, n: int, d: int, inner: int, dff: int) -> int:
-    return int(_lib.lib().jc_c2_layer_workspace_bytes(rows, n, d, inner, dff))
+def layer_workspace_bytes(rows: int, n: int, d: int, inner: int, dff: int, dtype: int = _lib.JC_F32) -> int:
+    return int(_lib.lib().jc_c2_layer_workspace_bytes(rows, n, d, inner, dff, dtype))
 
 
 def layer(x, weights: dict, live, table, group_start, group_end, workspace, rows: int, n: int, d: int, heads: int,
-          dh: int, dff: int, eps: float) -> None:
-    """One Chronos-2 encoder layer in place on x [rows*n, d] float32 (see include/jitcast_hip.h)."""
+          dh: int, dff: int, eps: float, dtype: int = _lib.JC_F32) -> None:
+    """One Chronos-2 encoder layer in place on x [rows*n, d] float32 (see include/jitcast_hip.h).
+
+    dtype JC_F32: fp32 weights. JC_BF16 / JC_F16: the weight matrices in that type (to_lp converts
+    them), norm weights and biases fp32; GEMMs and time attention in the storage type with fp32
+    accumulation, the residual stream fp32."""
     _f32(x, "x")
     ctx = context(x.device.index or 0)
     lw = LayerWeights.of(weights)
     _lib.call("jc_c2_layer", ctx.handle, _ptr(x), ctypes.byref(lw), _ptr(live), _ptr(table), _ptr(group_start),
-              _ptr(group_end), _ptr(workspace), rows, n, d, heads, dh, dff, ctypes.c_float(eps))
+              _ptr(group_end), _ptr(workspace), rows, n, d, heads, dh, dff, ctypes.c_float(eps), dtype)
+
+
+def linear_lp(a, w, c, bias=None, flags: int = 0, m: int | None = None, n: int | None = None, k: int | None = None,
+              lda: int | None = None, ldc: int | None = None) -> None:
+    """c (+)= act(a . w^T + bias): a and w bfloat16 or float16 (the same), c float32 or that type
+    (no GEMM_ACCUMULATE then); fp32 accumulation (Kernels.gemmHalf's contract)."""
+    dt = _dtype_code(a)
+    if dt == _lib.JC_F32 or _dtype_code(w) != dt:
+        raise _lib.JitcastArgumentError(_lib.JC_EINVAL, "a and w must both be bfloat16 or both float16")
+    m = a.shape[0] if m is None else m
+    n = w.shape[0] if n is None else n
+    k = w.shape[1] if k is None else k
+    lda = a.stride(0) if lda is None else lda
+    ldc = c.stride(0) if ldc is None else ldc
+    ctx = context(a.device.index or 0)
+    _lib.call("jc_linear_lp", ctx.handle, _ptr(a), lda, _ptr(w), _ptr(bias), _ptr(c), ldc, m, n, k, flags, dt,
+              _dtype_code(c))
+
+
+def rms_norm_lp(x, w, y, eps: float) -> None:
+    """y (bfloat16 or float16) = rmsNorm(x) with x float32 [rows, d]."""
+    _f32(x, "x")
+    ctx = context(x.device.index or 0)
+    rows, d = x.shape
+    _lib.call("jc_rms_norm_lp", ctx.handle, _ptr(x), _ptr(w), _ptr(y), rows, d, ctypes.c_float(eps), _dtype_code(y))
+
+
+def to_lp(src, dst) -> None:
+    """dst (bfloat16 or float16) = src (float32) rounded, saturated to the type's finite range."""
+    _f32(src, "src")
+    ctx = context(src.device.index or 0)
+    _lib.call("jc_to_lp", ctx.handle, _ptr(src), _ptr(dst), ctypes.c_int64(src.numel()), _dtype_code(dst))

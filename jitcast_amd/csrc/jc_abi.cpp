@@ -608,16 +608,26 @@ int jc_rms_norm(jc_ctx* ctx, const float* x, const float* w, float* y, int rows,
 
 static size_t round256(size_t b) { return (b + 255) & ~(size_t)255; }
 
-int64_t jc_c2_layer_workspace_bytes(int rows, int n, int d, int inner, int dff) {
+int64_t jc_c2_layer_workspace_bytes(int rows, int n, int d, int inner, int dff, int dtype) {
     if (rows < 0 || n < 0 || d < 0 || inner < 0 || dff < 0) return -1;
     const size_t t = (size_t)rows * n;
-    const size_t big = (size_t)(3 * inner > dff ? 3 * inner : dff);
-    return (int64_t)(round256(t * d * 4) + round256(t * big * 4) + round256(t * (size_t)inner * 4));
+    if (dtype == JC_F32) {
+        const size_t big = (size_t)(3 * inner > dff ? 3 * inner : dff);
+        return (int64_t)(round256(t * d * 4) + round256(t * big * 4) + round256(t * (size_t)inner * 4));
+    }
+    if (dtype != JC_BF16 && dtype != JC_F16) return -1;
+    const size_t big = (size_t)(12 * inner > 2 * dff ? 12 * inner : 2 * dff);  // bytes per token
+    return (int64_t)(round256(t * d * 2) + round256(t * big) + round256(t * (size_t)inner * 4) +
+                     round256(t * (size_t)inner * 2));
 }
+
+static int layer_lp(jc_ctx* ctx, const char* W, float* x, const jc_c2_layer_weights* w, const int32_t* live,
+                    const float* table, const int32_t* group_start, const int32_t* group_end, void* workspace, int rows,
+                    int n, int d, int heads, int dh, int dff, float eps, int dtype);
 
 int jc_c2_layer(jc_ctx* ctx, float* x, const jc_c2_layer_weights* w, const int32_t* live, const float* table,
                 const int32_t* group_start, const int32_t* group_end, void* workspace, int rows, int n, int d, int heads,
-                int dh, int dff, float eps) {
+                int dh, int dff, float eps, int dtype) {
     const char* W = "jc_c2_layer";
     int rc = use(ctx, W);
     if (rc) return rc;
@@ -633,6 +643,10 @@ int jc_c2_layer(jc_ctx* ctx, float* x, const jc_c2_layer_weights* w, const int32
     if (!w->time_norm || !w->time_qkv || !w->time_o || !w->group_norm || !w->group_qkv || !w->group_o ||
         !w->mlp_norm || !w->wi || !w->wo)
         return fail(JC_EINVAL, "%s: a null weight matrix or norm", W);
+    if (dtype == JC_BF16 || dtype == JC_F16)
+        return layer_lp(ctx, W, x, w, live, table, group_start, group_end, workspace, rows, n, d, heads, dh, dff, eps,
+                        dtype);
+    if (dtype != JC_F32) return fail(JC_EINVAL, "%s: dtype must be JC_F32, JC_BF16 or JC_F16 (got %d)", W, dtype);
     const int inner = heads * dh, T = rows * n;
     const size_t big_cols = (size_t)(3 * inner > dff ? 3 * inner : dff);
     char* ws = static_cast<char*>(workspace);
@@ -642,22 +656,138 @@ int jc_c2_layer(jc_ctx* ctx, float* x, const jc_c2_layer_weights* w, const int32
 
     // time attention sub-layer (Chronos2Forward.java:260-271)
     if ((rc = launch_rms(ctx, W, x, w->time_norm, hn, T, d, eps))) return rc;
-    if ((rc = launch_linear(ctx, W, hn, d, w->time_qkv, w->time_qkv_bias, big, 3 * inner, T, 3 * inner, d, 0))) return rc;
+    if ((rc = launch_linear(ctx, W, hn, d, static_cast<const float*>(w->time_qkv), w->time_qkv_bias, big, 3 * inner, T, 3 * inner, d, 0))) return rc;
     if ((rc = jc_c2_time_attention(ctx, big, att, live, table, rows, n, heads, dh, inner, JC_F32))) return rc;
-    if ((rc = launch_linear(ctx, W, att, inner, w->time_o, w->time_o_bias, x, d, T, d, inner, JC_GEMM_ACCUMULATE)))
+    if ((rc = launch_linear(ctx, W, att, inner, static_cast<const float*>(w->time_o), w->time_o_bias, x, d, T, d, inner, JC_GEMM_ACCUMULATE)))
         return rc;
     // group attention sub-layer (Chronos2Forward.java:273-281)
     if ((rc = launch_rms(ctx, W, x, w->group_norm, hn, T, d, eps))) return rc;
-    if ((rc = launch_linear(ctx, W, hn, d, w->group_qkv, w->group_qkv_bias, big, 3 * inner, T, 3 * inner, d, 0)))
+    if ((rc = launch_linear(ctx, W, hn, d, static_cast<const float*>(w->group_qkv), w->group_qkv_bias, big, 3 * inner, T, 3 * inner, d, 0)))
         return rc;
     if ((rc = jc_c2_group_attention(ctx, big, att, live, group_start, group_end, rows, n, heads, dh, inner, JC_F32)))
         return rc;
-    if ((rc = launch_linear(ctx, W, att, inner, w->group_o, w->group_o_bias, x, d, T, d, inner, JC_GEMM_ACCUMULATE)))
+    if ((rc = launch_linear(ctx, W, att, inner, static_cast<const float*>(w->group_o), w->group_o_bias, x, d, T, d, inner, JC_GEMM_ACCUMULATE)))
         return rc;
     // feed-forward sub-layer (Chronos2Forward.java:283-286)
     if ((rc = launch_rms(ctx, W, x, w->mlp_norm, hn, T, d, eps))) return rc;
-    if ((rc = launch_linear(ctx, W, hn, d, w->wi, w->wi_bias, big, dff, T, dff, d, JC_GEMM_RELU))) return rc;
-    return launch_linear(ctx, W, big, dff, w->wo, w->wo_bias, x, d, T, d, dff, JC_GEMM_ACCUMULATE);
+    if ((rc = launch_linear(ctx, W, hn, d, static_cast<const float*>(w->wi), w->wi_bias, big, dff, T, dff, d, JC_GEMM_RELU))) return rc;
+    return launch_linear(ctx, W, big, dff, static_cast<const float*>(w->wo), w->wo_bias, x, d, T, d, dff, JC_GEMM_ACCUMULATE);
+}
+
+// ---- bf16 / fp16 layer ------------------------------------------------------------------------
+
+static int check_lp_dtype(const char* W, int dtype) {
+    if (dtype != JC_BF16 && dtype != JC_F16) return fail(JC_EINVAL, "%s: dtype must be JC_BF16 or JC_F16 (got %d)", W, dtype);
+    return JC_OK;
+}
+
+static int launch_linear_lp(jc_ctx* ctx, const char* W, const void* a, int lda, const void* w, const float* bias,
+                            void* c, int ldc, int m, int n, int k, int flags, int dtype, int c_dtype) {
+    int rc = check_lp_dtype(W, dtype);
+    if (rc) return rc;
+    if (bias) flags |= JC_GEMM_BIAS;
+    if (m < 0 || n < 0 || k < 0) return fail(JC_EINVAL, "%s: negative size (m=%d n=%d k=%d)", W, m, n, k);
+    if ((size_t)m * n == 0) return JC_OK;
+    if (!a || !w || !c) return fail(JC_EINVAL, "%s: null a, w or c", W);
+    if (c_dtype != JC_F32 && c_dtype != dtype)
+        return fail(JC_EINVAL, "%s: c_dtype must be JC_F32 or the input dtype (got %d)", W, c_dtype);
+    if (k % 8 || k == 0) return fail(JC_EINVAL, "%s: k must be a positive multiple of 8 (got %d)", W, k);
+    if (lda < k || lda % 8) return fail(JC_EINVAL, "%s: lda must be >= k and a multiple of 8 (got %d)", W, lda);
+    if (ldc < n) return fail(JC_EINVAL, "%s: ldc must be >= n (got %d)", W, ldc);
+    if (!aligned16(a) || !aligned16(w)) return fail(JC_EINVAL, "%s: a and w must be 16-byte aligned", W);
+    if (flags & ~(JC_GEMM_BIAS | JC_GEMM_ACCUMULATE | JC_GEMM_SILU | JC_GEMM_RELU))
+        return fail(JC_EINVAL, "%s: unknown flags 0x%x", W, flags);
+    if ((flags & JC_GEMM_SILU) && (flags & JC_GEMM_RELU)) return fail(JC_EINVAL, "%s: SILU and RELU together", W);
+    if (c_dtype != JC_F32 && (flags & JC_GEMM_ACCUMULATE))
+        return fail(JC_EINVAL, "%s: JC_GEMM_ACCUMULATE needs an fp32 C", W);
+    jc::GemmLpArgs g{a, w, bias, c, m, n, k, lda, ldc, flags};
+    hipError_t e = jc::gemm_lp_launch(g, dtype == JC_F16, c_dtype != JC_F32, ctx->stream);
+    return e == hipSuccess ? JC_OK : hip_fail(W, e);
+}
+
+int jc_linear_lp(jc_ctx* ctx, const void* a, int lda, const void* w, const float* bias, void* c, int ldc, int m, int n,
+                 int k, int flags, int dtype, int c_dtype) {
+    const char* W = "jc_linear_lp";
+    int rc = use(ctx, W);
+    if (rc) return rc;
+    return launch_linear_lp(ctx, W, a, lda, w, bias, c, ldc, m, n, k, flags, dtype, c_dtype);
+}
+
+static int launch_rms_lp(jc_ctx* ctx, const char* W, const float* x, const float* w, void* y, int rows, int d, float eps,
+                         int dtype) {
+    int rc = check_lp_dtype(W, dtype);
+    if (rc) return rc;
+    if (rows < 0 || d < 0) return fail(JC_EINVAL, "%s: negative size", W);
+    if ((size_t)rows * d == 0) return JC_OK;
+    if (!x || !y) return fail(JC_EINVAL, "%s: null x or y", W);
+    if (d % 4) return fail(JC_EINVAL, "%s: d must be a multiple of 4 (got %d)", W, d);
+    if (!aligned16(x) || !aligned16(y) || (w && !aligned16(w))) return fail(JC_EINVAL, "%s: 16-byte alignment", W);
+    hipError_t e = jc::rms_norm_lp_launch(x, y, w, rows, d, eps, dtype == JC_F16, ctx->stream);
+    return e == hipSuccess ? JC_OK : hip_fail(W, e);
+}
+
+int jc_rms_norm_lp(jc_ctx* ctx, const float* x, const float* w, void* y, int rows, int d, float eps, int dtype) {
+    const char* W = "jc_rms_norm_lp";
+    int rc = use(ctx, W);
+    if (rc) return rc;
+    return launch_rms_lp(ctx, W, x, w, y, rows, d, eps, dtype);
+}
+
+static int launch_to_lp(jc_ctx* ctx, const char* W, const float* src, void* dst, int64_t count, int dtype) {
+    int rc = check_lp_dtype(W, dtype);
+    if (rc) return rc;
+    if (count < 0) return fail(JC_EINVAL, "%s: negative count", W);
+    if (count == 0) return JC_OK;
+    if (!src || !dst) return fail(JC_EINVAL, "%s: null src or dst", W);
+    hipError_t e = jc::to_lp_launch(src, dst, (uint64_t)count, dtype == JC_F16, ctx->stream);
+    return e == hipSuccess ? JC_OK : hip_fail(W, e);
+}
+
+int jc_to_lp(jc_ctx* ctx, const float* src, void* dst, int64_t count, int dtype) {
+    const char* W = "jc_to_lp";
+    int rc = use(ctx, W);
+    if (rc) return rc;
+    return launch_to_lp(ctx, W, src, dst, count, dtype);
+}
+
+static int layer_lp(jc_ctx* ctx, const char* W, float* x, const jc_c2_layer_weights* w, const int32_t* live,
+                    const float* table, const int32_t* group_start, const int32_t* group_end, void* workspace, int rows,
+                    int n, int d, int heads, int dh, int dff, float eps, int dtype) {
+    const int inner = heads * dh, T = rows * n;
+    const size_t t = (size_t)T;
+    const size_t big_bytes = (size_t)(12 * inner > 2 * dff ? 12 * inner : 2 * dff);
+    char* ws = static_cast<char*>(workspace);
+    void* hn = ws;                                                   // [T, d] storage type
+    void* big = ws + round256(t * d * 2);                            // qkv [T, 3*inner] (storage type or fp32) or act [T, dff]
+    float* att32 = reinterpret_cast<float*>(ws + round256(t * d * 2) + round256(t * big_bytes));  // [T, inner] fp32
+    void* att = ws + round256(t * d * 2) + round256(t * big_bytes) + round256(t * (size_t)inner * 4);  // [T, inner]
+    int rc;
+    // time attention sub-layer (Chronos2Forward.java:260-271), qkv and att in the storage type
+    if ((rc = launch_rms_lp(ctx, W, x, w->time_norm, hn, T, d, eps, dtype))) return rc;
+    if ((rc = launch_linear_lp(ctx, W, hn, d, w->time_qkv, w->time_qkv_bias, big, 3 * inner, T, 3 * inner, d, 0, dtype,
+                               dtype)))
+        return rc;
+    if ((rc = jc_c2_time_attention(ctx, big, att, live, table, rows, n, heads, dh, inner, dtype))) return rc;
+    if ((rc = launch_linear_lp(ctx, W, att, inner, w->time_o, w->time_o_bias, x, d, T, d, inner, JC_GEMM_ACCUMULATE,
+                               dtype, JC_F32)))
+        return rc;
+    // group attention sub-layer (Chronos2Forward.java:273-281): the group attention is fp32, so its
+    // qkv comes out of the GEMM in fp32 and its output is rounded once for the O projection
+    if ((rc = launch_rms_lp(ctx, W, x, w->group_norm, hn, T, d, eps, dtype))) return rc;
+    if ((rc = launch_linear_lp(ctx, W, hn, d, w->group_qkv, w->group_qkv_bias, big, 3 * inner, T, 3 * inner, d, 0,
+                               dtype, JC_F32)))
+        return rc;
+    if ((rc = jc_c2_group_attention(ctx, big, att32, live, group_start, group_end, rows, n, heads, dh, inner, JC_F32)))
+        return rc;
+    if ((rc = launch_to_lp(ctx, W, att32, att, (int64_t)t * inner, dtype))) return rc;
+    if ((rc = launch_linear_lp(ctx, W, att, inner, w->group_o, w->group_o_bias, x, d, T, d, inner, JC_GEMM_ACCUMULATE,
+                               dtype, JC_F32)))
+        return rc;
+    // feed-forward sub-layer (Chronos2Forward.java:283-286)
+    if ((rc = launch_rms_lp(ctx, W, x, w->mlp_norm, hn, T, d, eps, dtype))) return rc;
+    if ((rc = launch_linear_lp(ctx, W, hn, d, w->wi, w->wi_bias, big, dff, T, dff, d, JC_GEMM_RELU, dtype, dtype)))
+        return rc;
+    return launch_linear_lp(ctx, W, big, dff, w->wo, w->wo_bias, x, d, T, d, dff, JC_GEMM_ACCUMULATE, dtype, JC_F32);
 }
 
 }  // extern "C"

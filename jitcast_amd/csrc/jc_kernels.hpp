@@ -59,4 +59,21 @@ hipError_t gemm_f32_launch(const GemmArgs& g, hipStream_t stream);
 // y = x * (1 / sqrt(mean(x^2) + eps)) * w per row of d (d a multiple of 4; w may be null)
 hipError_t rms_norm_f32_launch(const float* x, float* y, const float* w, int rows, int d, float eps, hipStream_t stream);
 
+// bf16/fp16 GEMM with fp32 accumulation: C (+)= act(A . W^T + b), A [m, lda] and W [n, k] in the
+// storage type, C fp32 (out_lp false: any flags) or the storage type (out_lp true: no ACCUMULATE),
+// saturated to its finite range. k a multiple of 8; a, w 16-byte aligned, lda a multiple of 8.
+struct GemmLpArgs {
+    const void* a;
+    const void* w;
+    const float* bias;
+    void* c;
+    int m, n, k, lda, ldc, flags;
+};
+hipError_t gemm_lp_launch(const GemmLpArgs& g, bool fp16, bool out_lp, hipStream_t stream);
+// y (storage type) = x * (1 / sqrt(mean(x^2) + eps)) * w per row of d (d a multiple of 4)
+hipError_t rms_norm_lp_launch(const float* x, void* y, const float* w, int rows, int d, float eps, bool fp16,
+                              hipStream_t stream);
+// y[i] = x[i] rounded to the storage type, saturated to its finite range
+hipError_t to_lp_launch(const float* x, void* y, uint64_t count, bool fp16, hipStream_t stream);
+
 }  // namespace jc

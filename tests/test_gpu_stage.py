@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 import torch
 
-from jitcast_amd import JitcastArgumentError, chronos2
+from jitcast_amd import JitcastArgumentError, _lib, chronos2
 from tests import cases
 from tests.test_oracle_ops import _layer_weights
 
@@ -78,17 +78,27 @@ def test_rms_norm_matches_oracle(gpu, oracle, rows, d):
     assert oracle.rel_max_error(y.cpu().numpy(), oracle.rms_norm(x, w, 1e-6)) <= 1e-5
 
 
-def _run_layer(x, w, live, group, rows, n, heads, dh, dff, eps):
+MATRICES = ("time_qkv", "time_o", "group_qkv", "group_o", "wi", "wo")
+
+
+def _run_layer(x, w, live, group, rows, n, heads, dh, dff, eps, dtype=None):
     d = x.shape[1]
     inner = heads * dh
     xt = _t(x)
     wt = {k: _t(v) for k, v in w.items()}
+    code = _lib.JC_F32
+    if dtype is not None:  # the weight matrices in the storage type, converted on the device
+        code = {torch.bfloat16: _lib.JC_BF16, torch.float16: _lib.JC_F16}[dtype]
+        for k in MATRICES:
+            lp = torch.empty(wt[k].shape, dtype=dtype, device=DEV)
+            chronos2.to_lp(wt[k], lp)
+            wt[k] = lp
     gs, ge = chronos2.group_bounds(group)
     table = _t(chronos2.rope_table(n, dh))
-    nbytes = chronos2.layer_workspace_bytes(rows, n, d, inner, dff)
+    nbytes = chronos2.layer_workspace_bytes(rows, n, d, inner, dff, code)
     ws = torch.empty(nbytes // 4 + 64, device=DEV)
     chronos2.layer(xt, wt, _t(live.reshape(-1).astype(np.int32)), table, _t(gs), _t(ge), ws, rows, n, d, heads, dh,
-                   dff, eps)
+                   dff, eps, code)
     torch.cuda.synchronize()
     return xt.cpu().numpy()
 
@@ -113,6 +123,77 @@ def test_layer_matches_oracle(gpu, oracle, rows, n, heads, dh, d, dff, bias):
     assert err <= TOL
 
 
+LP = {"bf16": torch.bfloat16, "fp16": torch.float16}
+
+
+@pytest.mark.parametrize("dt", sorted(LP))
+@pytest.mark.parametrize("m,n,k", [(1, 16, 16), (37, 100, 64), (300, 257, 776), (513, 256, 768)])
+@pytest.mark.parametrize("flags,bias,out", [(0, False, "lp"), (chronos2.GEMM_RELU, True, "lp"), (0, True, "f32"),
+                                            (chronos2.GEMM_ACCUMULATE, False, "f32"),
+                                            (chronos2.GEMM_RELU | chronos2.GEMM_ACCUMULATE, True, "f32")])
+def test_linear_lp_matches_oracle(gpu, oracle, m, n, k, flags, bias, out, dt):
+    """bf16/fp16 GEMM: exact to fp32-accumulation rounding of the rounded operands (the oracle on
+    the same rounded values), then rounded to the output type."""
+    print(f"case {dt} m={m} n={n} k={k} flags={flags} bias={bias} out={out}", flush=True)
+    r = np.random.default_rng(m + n + k + flags)
+    a = r.standard_normal((m, k)).astype(np.float32)
+    w = (r.standard_normal((n, k)) / np.sqrt(k)).astype(np.float32)
+    b = r.standard_normal(n).astype(np.float32) if bias else None
+    c0 = r.standard_normal((m, n)).astype(np.float32)
+    at, wt = _t(a).to(LP[dt]), _t(w).to(LP[dt])
+    c = _t(c0) if out == "f32" else torch.empty(m, n, dtype=LP[dt], device=DEV)
+    chronos2.linear_lp(at, wt, c, bias=_t(b) if bias else None, flags=flags)
+    torch.cuda.synchronize()
+    exp = _epilogue(oracle.linear(at.float().cpu().numpy(), wt.float().cpu().numpy()), c0, b, flags)
+    got = c.float().cpu().numpy()
+    tol = 1e-5 if out == "f32" else 2 ** -8  # one rounding to the storage type
+    assert oracle.rel_max_error(got, exp) <= tol
+
+
+@pytest.mark.parametrize("dt", sorted(LP))
+def test_rms_norm_lp_and_to_lp(gpu, oracle, dt):
+    r = np.random.default_rng(4)
+    x = (3 * r.standard_normal((77, 768))).astype(np.float32)
+    w = r.standard_normal(768).astype(np.float32)
+    y = torch.empty(77, 768, dtype=LP[dt], device=DEV)
+    chronos2.rms_norm_lp(_t(x), _t(w), y, 1e-6)
+    big = np.array([1e30, -1e30, 7e4, -7e4, 1.5, np.nan, 0.0, -2.5], np.float32)
+    z = torch.empty(8, dtype=LP[dt], device=DEV)
+    chronos2.to_lp(_t(big), z)
+    torch.cuda.synchronize()
+    exp = oracle.rms_norm(x, w, 1e-6)
+    # one rounding of the fp32 norm (the sums differ in order from the oracle's: at most one ulp of T)
+    assert oracle.rel_max_error(y.float().cpu().numpy(), exp) <= 2 ** -8
+    zz = z.float().cpu().numpy()
+    finite_max = float(torch.finfo(LP[dt]).max)
+    assert zz[0] <= finite_max and zz[1] >= -finite_max and np.isfinite(zz[[0, 1, 2, 3]]).all()  # saturated
+    assert np.isnan(zz[5]) and zz[4] == 1.5 and zz[7] == -2.5
+
+
+@pytest.mark.parametrize("dt", sorted(LP))
+@pytest.mark.parametrize("rows,n,heads,dh,d,dff", [(6, 37, 4, 16, 64, 128), (3, 260, 12, 64, 768, 3072)])
+def test_layer_lp_matches_fp32_oracle(gpu, oracle, rows, n, heads, dh, d, dff, dt):
+    """The bf16/fp16 layer against the fp32 oracle on the unrounded weights and inputs, at the
+    bf16/fp16 bar (2e-2)."""
+    print(f"case {dt} rows={rows} n={n} heads={heads} dh={dh} d={d} dff={dff}", flush=True)
+    # the benchmark configurations' initialisation (weights N(0, 0.02), norms 1 +- 0.1, biases 0.1):
+    # unscaled Chronos-2 scores then have a std of about 2.5 (with 1/sqrt(in) weights they reach 8,
+    # and bf16's 8-bit mantissa alone moves such a softmax by a few percent)
+    w = _layer_weights(31 + d, d, heads * dh, dff, True)
+    r = np.random.default_rng(35)
+    for k in MATRICES:
+        w[k] = (0.02 * r.standard_normal(w[k].shape)).astype(np.float32)
+    x = np.random.default_rng(32).standard_normal((rows * n, d)).astype(np.float32)
+    live = cases.left_pad_live(33, rows, n, n // 3)
+    group = np.sort(np.random.default_rng(34).integers(0, max(1, rows // 2), rows)).astype(np.int32)
+    got = _run_layer(x, w, live, group, rows, n, heads, dh, dff, 1e-6, LP[dt])
+    exp = oracle.c2_layer(x, w, live, group, rows, n, heads, dh, 1e-6)
+    err = oracle.rel_max_error(got, exp)
+    print(f"  rel err {err:.3e}", flush=True)
+    assert np.isfinite(got).all()
+    assert err <= 2e-2
+
+
 def test_layer_rejects_bad_arguments(gpu):
     x = torch.zeros(10, 64, device=DEV)
     with pytest.raises(JitcastArgumentError):
@@ -127,3 +208,7 @@ def test_layer_rejects_bad_arguments(gpu):
     ws = torch.zeros(1024, device=DEV)
     with pytest.raises(JitcastArgumentError):  # dh past 64
         chronos2.layer(x, w, None, None, None, None, ws, 1, 10, 64, 1, 80, 128, 1e-6)
+    with pytest.raises(JitcastArgumentError):  # ACCUMULATE into a bf16 C
+        xb = x.to(torch.bfloat16)
+        chronos2.linear_lp(xb, torch.zeros(8, 64, dtype=torch.bfloat16, device=DEV),
+                           torch.zeros(10, 8, dtype=torch.bfloat16, device=DEV), flags=chronos2.GEMM_ACCUMULATE)
