@@ -351,6 +351,33 @@ int jc_rms_norm_lp(jc_ctx *ctx, const float *x, const float *w, void *y, int row
  * J/tornado/Kernels.java:887-895): for weights, converted once. */
 int jc_to_lp(jc_ctx *ctx, const float *src, void *dst, int64_t count, int dtype);
 
+/* ---- The rest of the Chronos-2 forward (fp32) ------------------------------------------------ */
+
+/*
+ * x [rows*n, d]: the encoder input from the patch embeddings emb [rows*(n-nreg), d] (each row's
+ * context tokens then its future tokens) and the [REG] token reg [d] between them (NULL when
+ * nreg = 0): Chronos2Kernels.assembleTokens (J/chronos2/tornado/Chronos2Kernels.java:66-85).
+ * 0 <= nc, 0 <= nreg <= 1, nc + nreg <= n; d a multiple of 4; 16-byte aligned.
+ */
+int jc_c2_assemble(jc_ctx *ctx, const float *emb, const float *reg, float *x, int rows, int nc, int nreg, int n, int d);
+
+/*
+ * dec [rows*h, d] = the tokens fs..fs+h-1 of every row of y [rows*n, d]: Chronos2Kernels.gatherFuture
+ * (J/chronos2/tornado/Chronos2Kernels.java:684-694). fs + h <= n; d a multiple of 4; 16-byte aligned.
+ */
+int jc_c2_gather_future(jc_ctx *ctx, const float *y, float *dec, int rows, int fs, int n, int h, int d);
+
+/*
+ * out [m, dout] = output(ReLU(hidden(x))) + residual(x): a Chronos-2 residual block (the input and
+ * output patch embeddings), as Chronos2Forward.Plan.residual queues it
+ * (J/chronos2/tornado/Chronos2Forward.java:306-311; CPU CpuChronos2.Residual.apply,
+ * J/chronos2/cpu/CpuChronos2.java:57-69). x [m, din]; hidden [dff, din], output [dout, dff],
+ * residual [dout, din] with optional fp32 biases; scratch [m, dff]. din, dff multiples of 16.
+ */
+int jc_c2_residual(jc_ctx *ctx, const float *x, int m, int din, const float *w_hidden, const float *b_hidden,
+                   const float *w_output, const float *b_output, const float *w_residual, const float *b_residual,
+                   int dff, int dout, float *scratch, float *out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -79,6 +79,9 @@ SIGNATURES = {
     "jc_linear_lp": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i]),
     "jc_rms_norm_lp": (_i, [_vp, _vp, _vp, _vp, _i, _i, _f, _i]),
     "jc_to_lp": (_i, [_vp, _vp, _vp, _c.c_int64, _i]),
+    "jc_c2_assemble": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i]),
+    "jc_c2_gather_future": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i]),
+    "jc_c2_residual": (_i, [_vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp]),
     "jc_ts_block_layout": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _c.POINTER(_i), _c.POINTER(_i), _vp,
                                 _vp, _vp]),
 }

@@ -790,4 +790,48 @@ static int layer_lp(jc_ctx* ctx, const char* W, float* x, const jc_c2_layer_weig
     return launch_linear_lp(ctx, W, big, dff, w->wo, w->wo_bias, x, d, T, d, dff, JC_GEMM_ACCUMULATE, dtype, JC_F32);
 }
 
+// ---- The rest of the Chronos-2 forward ------------------------------------------------------
+
+int jc_c2_assemble(jc_ctx* ctx, const float* emb, const float* reg, float* x, int rows, int nc, int nreg, int n, int d) {
+    const char* W = "jc_c2_assemble";
+    int rc = use(ctx, W);
+    if (rc) return rc;
+    if (rows < 0 || nc < 0 || nreg < 0 || nreg > 1 || nc + nreg > n || d <= 0)
+        return fail(JC_EINVAL, "%s: sizes (rows=%d nc=%d nreg=%d n=%d d=%d)", W, rows, nc, nreg, n, d);
+    if ((size_t)rows * n == 0) return JC_OK;
+    if (d % 4) return fail(JC_EINVAL, "%s: d must be a multiple of 4 (got %d)", W, d);
+    if (!x || (n > nreg && !emb) || (nreg && !reg)) return fail(JC_EINVAL, "%s: null buffer", W);
+    if (!aligned16(x) || (emb && !aligned16(emb)) || (reg && !aligned16(reg)))
+        return fail(JC_EINVAL, "%s: 16-byte alignment", W);
+    hipError_t e = jc::assemble_tokens_launch(emb, reg, x, rows, nc, nreg, n, d, ctx->stream);
+    return e == hipSuccess ? JC_OK : hip_fail(W, e);
+}
+
+int jc_c2_gather_future(jc_ctx* ctx, const float* y, float* dec, int rows, int fs, int n, int h, int d) {
+    const char* W = "jc_c2_gather_future";
+    int rc = use(ctx, W);
+    if (rc) return rc;
+    if (rows < 0 || fs < 0 || h < 0 || fs + h > n || d <= 0)
+        return fail(JC_EINVAL, "%s: sizes (rows=%d fs=%d h=%d n=%d d=%d)", W, rows, fs, h, n, d);
+    if ((size_t)rows * h == 0) return JC_OK;
+    if (d % 4) return fail(JC_EINVAL, "%s: d must be a multiple of 4 (got %d)", W, d);
+    if (!y || !dec) return fail(JC_EINVAL, "%s: null buffer", W);
+    if (!aligned16(y) || !aligned16(dec)) return fail(JC_EINVAL, "%s: 16-byte alignment", W);
+    hipError_t e = jc::gather_future_launch(y, dec, rows, fs, n, h, d, ctx->stream);
+    return e == hipSuccess ? JC_OK : hip_fail(W, e);
+}
+
+int jc_c2_residual(jc_ctx* ctx, const float* x, int m, int din, const float* w_hidden, const float* b_hidden,
+                   const float* w_output, const float* b_output, const float* w_residual, const float* b_residual, int dff,
+                   int dout, float* scratch, float* out) {
+    const char* W = "jc_c2_residual";
+    int rc = use(ctx, W);
+    if (rc) return rc;
+    if (!scratch || !w_hidden || !w_output || !w_residual) return fail(JC_EINVAL, "%s: null weight or scratch", W);
+    // Plan.residual: hidden with ReLU into scratch, output into out, residual accumulated into out
+    if ((rc = launch_linear(ctx, W, x, din, w_hidden, b_hidden, scratch, dff, m, dff, din, JC_GEMM_RELU))) return rc;
+    if ((rc = launch_linear(ctx, W, scratch, dff, w_output, b_output, out, dout, m, dout, dff, 0))) return rc;
+    return launch_linear(ctx, W, x, din, w_residual, b_residual, out, dout, m, dout, din, JC_GEMM_ACCUMULATE);
+}
+
 }  // extern "C"

@@ -76,4 +76,10 @@ hipError_t rms_norm_lp_launch(const float* x, void* y, const float* w, int rows,
 // y[i] = x[i] rounded to the storage type, saturated to its finite range
 hipError_t to_lp_launch(const float* x, void* y, uint64_t count, bool fp16, hipStream_t stream);
 
+// Chronos-2 token moves (d a multiple of 4, 16-byte aligned): the encoder input from the patch
+// embeddings and [REG] (reg may be null when nreg = 0), and the future tokens of the encoder output
+hipError_t assemble_tokens_launch(const float* emb, const float* reg, float* x, int rows, int nc, int nreg, int n, int d,
+                                  hipStream_t stream);
+hipError_t gather_future_launch(const float* y, float* dec, int rows, int fs, int n, int h, int d, hipStream_t stream);
+
 }  // namespace jc

@@ -185,6 +185,104 @@ def c2_layer(x, w: dict, live, group, rows, n, heads, dh, eps, theta=10000.0, th
     return add(x, linear(act, w["wo"], w.get("wo_bias"), threads))
 
 
+def c2_residual(x, w: dict, prefix: str, threads=0) -> np.ndarray:
+    """CpuChronos2.Residual.apply (CpuChronos2.java:57-69): output(ReLU(hidden(x))) + residual(x)."""
+    h = relu(linear(x, w[prefix + "_hidden_w"], w.get(prefix + "_hidden_b"), threads))
+    y = linear(h, w[prefix + "_output_w"], w.get(prefix + "_output_b"), threads)
+    return add(y, linear(x, w[prefix + "_residual_w"], w.get(prefix + "_residual_b"), threads))
+
+
+def c2_forward_raw(tokens, w: dict, live, group, rows, nc, nreg, h, heads, dh, eps, theta=10000.0,
+                   threads=0) -> np.ndarray:
+    """CpuChronos2.forward from the patch tokens to the raw output patch embedding
+    (CpuChronos2.java:122-169): the input embedding, the context / [REG] / future token order, the
+    encoder layers, the final RMSNorm, the future tokens, the output embedding. tokens
+    [rows*(nc+h), 3P]; w as jitcast_amd.chronos2_model.random_weights lays it out."""
+    ne, n = nc + h, nc + nreg + h
+    emb = c2_residual(tokens, w, "in", threads)
+    d = emb.shape[1]
+    x = np.empty((rows * n, d), np.float32)
+    for i in range(rows):
+        x[i * n: i * n + nc] = emb[i * ne: i * ne + nc]
+        if nreg:
+            x[i * n + nc] = w["shared"][1]
+        x[i * n + nc + nreg: (i + 1) * n] = emb[i * ne + nc: (i + 1) * ne]
+    for lw in w["layers"]:
+        x = c2_layer(x, lw, live, group, rows, n, heads, dh, eps, theta, threads)
+    y = rms_norm(x, w["final_norm"], eps)
+    dec = np.concatenate([y[i * n + nc + nreg: (i + 1) * n] for i in range(rows)])
+    return c2_residual(dec, w, "out", threads)
+
+
+def c2_instance_norm(row) -> tuple:
+    """ModelPrep.instanceNorm (ModelPrep.java:80-101), value by value: mean and population std of the
+    observed values in double, rounded to float; a zero std floored at 1e-5; (0, 1) with none."""
+    total, cnt = 0.0, 0
+    for v in row:
+        if not np.isnan(v):
+            total += float(v)
+            cnt += 1
+    if cnt == 0:
+        return np.float32(0), np.float32(1)
+    loc = np.float32(total / cnt)
+    ss = 0.0
+    for v in row:
+        if not np.isnan(v):
+            dv = np.float32(np.float32(v) - loc)
+            ss += float(dv) * float(dv)
+    scale = np.float32(np.sqrt(ss / cnt))
+    return loc, (np.float32(1e-5) if scale == 0 else scale)
+
+
+def _c2_scaled(v, loc, scale, arcsinh):
+    """ModelPrep.scaled / asinh (ModelPrep.java:104-114)."""
+    x = np.float32(np.float32(np.float32(v) - loc) / scale)
+    if not arcsinh:
+        return x
+    a = abs(float(x))
+    r = np.log(a + np.sqrt(a * a + 1.0))
+    return np.float32(-r if x < 0 else r)
+
+
+def c2_prep(window, future, nc, h, patch, time_scale, arcsinh):
+    """ModelPrep.of (ModelPrep.java:38-72), row by row: tokens [rows*(nc+h), 3P] of time encoding,
+    scaled value (0 where missing) and observation mask; loc, scale [rows]."""
+    rows = window.shape[0]
+    ps, ne = patch, nc + h
+    tok = np.zeros((rows * ne, 3 * ps), np.float32)
+    loc = np.zeros(rows, np.float32)
+    scale = np.zeros(rows, np.float32)
+    for i in range(rows):
+        loc[i], scale[i] = c2_instance_norm(window[i])
+        for p in range(ne):
+            for s in range(ps):
+                if p < nc:
+                    t = p * ps + s
+                    te, v = np.float32(np.float32(t - nc * ps) / np.float32(time_scale)), window[i][t]
+                else:
+                    t = (p - nc) * ps + s
+                    te, v = np.float32(np.float32(t) / np.float32(time_scale)), future[i][t]
+                obs = not np.isnan(v)
+                tok[i * ne + p, s] = te
+                tok[i * ne + p, ps + s] = _c2_scaled(v, loc[i], scale[i], arcsinh) if obs else np.float32(0)
+                tok[i * ne + p, 2 * ps + s] = 1.0 if obs else 0.0
+    return tok, loc, scale
+
+
+def c2_finish(raw, loc, scale, rows, h, q, patch, arcsinh) -> np.ndarray:
+    """ModelPrep.finish (ModelPrep.java:125-150): [rows, Q, h*P] = sinh(raw)*scale + loc."""
+    out = np.zeros((rows, q, h * patch), np.float32)
+    for i in range(rows):
+        for p in range(h):
+            for k in range(q):
+                for s in range(patch):
+                    v = np.float32(raw[i * h + p, k * patch + s])
+                    if arcsinh:
+                        v = np.float32(np.sinh(float(v)))
+                    out[i, k, p * patch + s] = np.float32(np.float32(v * scale[i]) + loc[i])
+    return out
+
+
 def rel_max_error(actual, expected) -> float:
     """The reference's metric: max|a-e| / max(max|e|, 1e-6); a NaN mismatch is infinite
     (T/chronos2/Chronos2Golden.java:218-234)."""
