@@ -241,6 +241,58 @@ def ts_time_attention_line(steps: int, warmup: int) -> dict:
     return res
 
 
+def forecast_line(steps: int, warmup: int, dtype_name: str = "f32") -> dict:
+    """Config 4 end to end: HipChronos2Model.forecast on 1024 groups x (4 series + 1 known-future
+    covariate) of 2048 steps, horizon 64, 21 quantiles, Chronos-2 120M-class random-init weights.
+    value = target series forecast per second, wall clock around forecast() (host layout and prep,
+    one upload, the device forward, one download, the inverse norm)."""
+    import numpy as np
+    import torch
+
+    from jitcast_amd import chronos2_model as cm, synthetic
+
+    c = cm.Chronos2Config()  # d_model 768, 12 x 64, 12 layers, d_ff 3072, patch 16, 21 quantiles
+    w = cm.random_weights(c, seed=0)
+    model = cm.HipChronos2Model(c, w, dtype=dtype_name)
+    del w
+    ctx, group, fut, targets = synthetic.c2_forecast_config4()
+    h = 64 // c.patch_size
+    for _ in range(warmup):
+        model.forecast(ctx, group, fut, h=h)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        out = model.forecast(ctx, group, fut, h=h)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / steps
+    # the device forward alone (prepared tokens resident), HIP events
+    lay = cm.layout(c, ctx, group, fut, h)
+    tok, _, _ = cm.prep(c, lay)
+    gs, ge = cm.chronos2.group_bounds(lay.group)
+    dev = model.dev
+    args = (torch.from_numpy(tok).to(dev), torch.from_numpy(lay.live.reshape(-1)).to(dev), torch.from_numpy(gs).to(dev),
+            torch.from_numpy(ge).to(dev), lay.rows, lay.nc, lay.h)
+    dev_ms = time_launches(lambda: model.forward_raw(*args), max(2, steps), 1)
+    series = int(targets.sum())
+    assert np.isfinite(out).all()
+    log(f"forecast {dtype_name}: {wall * 1e3:.1f} ms per call end to end ({series / wall:.0f} series/s), device "
+        f"forward {dev_ms:.1f} ms ({series / (dev_ms * 1e-3):.0f} series/s)")
+    res = {
+        "workload": f"config 4: Chronos-2 120M-class forecast ({dtype_name} encoder), 1024 groups x (4 series + 1 "
+                    "known-future covariate) x 2048 steps, horizon 64, 21 quantiles, random-init weights",
+        "metric": "forecast series/sec",
+        "value": round(series / wall, 1),
+        "unit": "series/s",
+        "ms_per_call": round(wall * 1e3, 2),
+        "device_forward_ms": round(dev_ms, 2),
+        "device_series_per_s": round(series / (dev_ms * 1e-3), 1),
+        "rows": lay.rows, "tokens_per_row": lay.n,
+    }
+    del model
+    torch.cuda.empty_cache()
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -248,7 +300,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=256)
-    ap.add_argument("--only", choices=["all", "time", "group", "bf16", "fp16", "layer", "layer-bf16", "ts"], default="all",
+    ap.add_argument("--only", choices=["all", "time", "group", "bf16", "fp16", "layer", "layer-bf16", "ts", "forecast"], default="all",
                     help="which workloads to run (profiling runs select one kernel)")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="only run 5 plain device copies of this many bytes (calibrates rocprof byte counters)")
@@ -275,6 +327,12 @@ def main() -> int:
         log(f"copied {args.copy_bytes} bytes 5 times")
         return 0
     also = {}
+    if args.only in ("all", "forecast"):
+        for name in ("bf16", "f32"):
+            also[f"c2_forecast_{name}"] = forecast_line(2, 1, name)
+        if args.only == "forecast":
+            print(json.dumps({"also": also}), flush=True)
+            return 0
     if args.only in ("all", "ts"):
         also["ts_time_attention_bf16"] = ts_time_attention_line(max(3, args.steps // 5), 1)
         if args.only == "ts":

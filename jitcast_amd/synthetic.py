@@ -212,3 +212,30 @@ def ts_time_config3(rows: int = 64, n: int = 1024, heads: int = 12, dh: int = 64
     table = torch.from_numpy(ts_rope_table(n, n, dh, rope_dim)).to(device)
     return TsTimeCase(rows, n, heads, dh, d, qkv, gate, torch.from_numpy(key_valid.reshape(-1)).to(device),
                       torch.from_numpy(known).to(device), torch.from_numpy(pos.reshape(-1)).to(device), table, starts)
+
+
+def c2_forecast_config4(groups: int = 1024, per_group: int = 4, t: int = 2048, horizon: int = 64, seed: int = 0):
+    """Config 4's forecast inputs (host arrays): each group holds `per_group` target series of `t`
+    steps (config 0's generator: sines of periods 24 and 168 with amplitudes U(0.5, 2), a linear
+    trend of slope U(-0.01, 0.01), N(0, 0.1) noise) and one known-future covariate row (N(0, 1) past
+    and `horizon` future steps). Returns (context [rows, t], group [rows], future [rows, horizon],
+    targets: the boolean mask of target rows)."""
+    r = np.random.default_rng(seed)
+    rows = groups * (per_group + 1)
+    steps = np.arange(t, dtype=np.float64)
+    ctx = np.empty((rows, t), np.float32)
+    fut = np.full((rows, horizon), np.nan, np.float32)
+    targets = np.ones(rows, bool)
+    for g in range(groups):
+        base = g * (per_group + 1)
+        for s in range(per_group):
+            a1, a2 = r.uniform(0.5, 2.0, 2)
+            slope = r.uniform(-0.01, 0.01)
+            ctx[base + s] = (a1 * np.sin(2 * np.pi * steps / 24) + a2 * np.sin(2 * np.pi * steps / 168) + slope * steps
+                             + r.normal(0, 0.1, t)).astype(np.float32)
+        cov = base + per_group
+        ctx[cov] = r.standard_normal(t).astype(np.float32)
+        fut[cov] = r.standard_normal(horizon).astype(np.float32)
+        targets[cov] = False
+    group = (np.arange(rows) // (per_group + 1)).astype(np.int32)
+    return ctx, group, fut, targets
