@@ -63,15 +63,18 @@ int use(jc_ctx* ctx, const char* where) {
 size_t dtype_size(int dtype) { return dtype == JC_F32 ? 4 : 2; }
 
 // JITCAST_HIP_LP_KERNEL picks the bf16/fp16 time-attention kernel: "stream" (time_attention_lp,
-// which takes every shape) or "wide" (time_attention_lpw, for the shapes it takes). Unset, Chronos-2
-// uses the row-wide kernel and Timestral the streaming one: its row-wide variant holds every
-// token's table row in LDS and fits one workgroup per CU (measured on config 3: 6.30 ms against
-// 6.04 ms per 12 layers). Read at every launch, so a host can switch at run time.
-bool lp_use_wide(bool ts) {
+// which takes every shape), "wide" (time_attention_lpw) or "persist" (time_attention_lpp), the
+// last two for the shapes they take. Unset, Chronos-2 uses the persistent kernel where it fits,
+// else the row-wide one, and Timestral the streaming one: its row-wide variant holds every token's
+// table row in LDS and fits one workgroup per CU (measured on config 3: 6.30 ms against 6.04 ms
+// per 12 layers). Read at every launch, so a host can switch at run time.
+enum LpKernel { kLpStream, kLpWide, kLpPersist };
+LpKernel lp_choice(bool ts) {
     const char* e = getenv("JITCAST_HIP_LP_KERNEL");
-    if (e && !strcmp(e, "stream")) return false;
-    if (e && !strcmp(e, "wide")) return true;
-    return !ts;
+    if (e && !strcmp(e, "stream")) return kLpStream;
+    if (e && !strcmp(e, "wide")) return kLpWide;
+    if (e && !strcmp(e, "persist")) return kLpPersist;
+    return ts ? kLpStream : kLpPersist;
 }
 
 }  // namespace
@@ -286,7 +289,9 @@ static int launch_time(jc_ctx* ctx, const char* W, const jc::TimeArgs& a, int dh
     const bool fp16 = dtype == JC_F16;
     if (dtype == JC_F32) {
         e = jc::time_attention_f32_launch(a, dh, ts, ctx->stream);
-    } else if (lp_use_wide(ts) && jc::time_attention_lpw_fits(a, dh)) {
+    } else if (lp_choice(ts) == kLpPersist && jc::time_attention_lpp_fits(a, dh, ts)) {
+        e = jc::time_attention_lpp_launch(a, fp16, ctx->cus, ctx->stream);
+    } else if (lp_choice(ts) != kLpStream && jc::time_attention_lpw_fits(a, dh)) {
         e = jc::time_attention_lpw_launch(a, dh, ts, fp16, ctx->stream);
     } else {
         e = jc::time_attention_lp_launch(a, dh, ts, fp16, ctx->stream);

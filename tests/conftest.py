@@ -41,12 +41,13 @@ def gpu():
     return ctx
 
 
-@pytest.fixture(params=["stream", "wide"])
+@pytest.fixture(params=["stream", "wide", "persist"])
 def lp_kernel(request, monkeypatch):
     """Which bf16/fp16 time-attention kernel the library launches (JITCAST_HIP_LP_KERNEL): the
-    streaming one, or the row-wide one (rows of 256+ tokens and head width 32 or 64; other shapes
-    fall back to the streaming kernel). Unset, Chronos-2 uses the row-wide kernel, Timestral the
-    streaming one."""
+    streaming one, the row-wide one (rows of 256+ tokens and head width 32 or 64) or the persistent
+    one (Chronos-2 rows of 257..513 tokens, head width 64); a shape the chosen kernel does not take
+    falls back to the row-wide or streaming kernel. Unset, Chronos-2 uses the persistent kernel
+    where it fits, Timestral the streaming one."""
     monkeypatch.setenv("JITCAST_HIP_LP_KERNEL", request.param)
     return request.param
 

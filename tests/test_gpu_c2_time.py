@@ -68,6 +68,9 @@ def test_fp32_matches_oracle(gpu, oracle, rows, n, heads, dh, inner, kind):
 LP_CASES = [c for c in CASES if c[3] % 16 == 0 and c[4] % 8 == 0] + [
     (2, 513, 2, 64, 128, "pad"),
     (1, 1030, 1, 64, 64, "random"),
+    (3, 300, 2, 64, 136, "random"),
+    (1, 257, 1, 64, 64, "pad"),
+    (2, 512, 3, 64, 192, "random"),
 ]
 
 
@@ -232,3 +235,53 @@ def test_rejects_bad_shapes(gpu):
         chronos2.time_attention(q, o, lv, 1, 4, 1, 12, 64)
     with pytest.raises(JitcastArgumentError, match="inner"):
         chronos2.time_attention(q, o, lv, 1, 4, 2, 64, 64)
+
+
+@pytest.mark.parametrize("dt", sorted(LP_DTYPES))
+@pytest.mark.parametrize("table", [True, False])
+def test_lowp_many_items_per_workgroup(gpu, oracle, dt, table, monkeypatch):
+    """The persistent kernel walks up to 12 (row, head) items per workgroup and streams their blocks
+    back to back: 300 rows x 12 heads at n = 513 gives every workgroup 12 items of different lengths,
+    including a row without live keys (zeros), a row whose only live key is [REG], rows with gaps
+    and left-padded rows. Without a table the kernel takes q and k as already rotated."""
+    monkeypatch.setenv("JITCAST_HIP_LP_KERNEL", "persist")
+    rows, n, heads, dh = 300, 513, 12, 64
+    inner = heads * dh
+    print(f"case {dt} persist many items table={table} rows={rows} n={n}", flush=True)
+    qkv = cases.qkv(61, rows * n, inner, std=0.554)
+    live = cases.left_pad_live(61, rows, n, 256)
+    gaps = cases.random_live(61, rows, n, 0.7)
+    live[::3] = gaps[::3]
+    live[:, n - 1] = 1
+    live[5] = 0
+    live[7] = 0
+    live[7, n - 1] = 1
+    live[11, :64] = 1
+    live[11, 64:n - 1] = 0
+    got = _run(qkv, live, rows, n, heads, dh, inner, table=table, dtype=LP_DTYPES[dt])
+    assert np.isfinite(got).all()
+    assert not np.any(got.reshape(rows, n, inner)[5])
+    rounded = torch.from_numpy(qkv).to(LP_DTYPES[dt]).float().numpy()
+    if table:
+        exp = oracle.c2_time_attention(rounded, live, rows, n, heads, dh, inner)
+        err = oracle.rel_max_error(got, exp)
+    else:
+        # rows of the first and the last item of every workgroup, and the special rows
+        pick = np.r_[0:16, 5, 7, 11, 280:300]
+        exp = _plain_attention(rounded, live, pick, n, heads, dh, inner)
+        err = oracle.rel_max_error(got.reshape(rows, n, inner)[pick].reshape(-1, inner), exp)
+    print(f"  rel err vs the reference on the rounded inputs {err:.3e}", flush=True)
+    assert err <= TOL_LP / 2
+
+
+def _plain_attention(qkv, live, pick, n, heads, dh, inner):
+    """float64 masked attention without RoPE or scale on the rows `pick` (torch on the CPU)."""
+    x = torch.from_numpy(qkv).double().reshape(-1, n, 3 * inner)[torch.from_numpy(np.asarray(pick))]
+    q, k, v = (x[:, :, i * inner:(i + 1) * inner].reshape(len(pick), n, heads, dh).transpose(1, 2).contiguous()
+               for i in range(3))
+    s = torch.matmul(q, k.transpose(-1, -2).contiguous())
+    m = torch.from_numpy(live[pick] == 1)[:, None, None, :]
+    s = s.masked_fill(~m, float("-inf"))
+    p = torch.softmax(s, -1).nan_to_num(0.0)
+    o = torch.matmul(p, v).transpose(1, 2).reshape(len(pick) * n, inner)
+    return o.numpy()
