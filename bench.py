@@ -137,7 +137,7 @@ def time_attention_lowp_line(case, steps: int, warmup: int, dtype_name: str) -> 
         f"({100 * tf / PEAK_BF16_TFLOPS:.1f}% of the {dtype_name} MFMA peak)")
     res = {
         "workload": f"config 1-{dtype_name}: the config-1 inputs with qkv in {dtype_name}, fp32 accumulation",
-        "kernel": "jc::time_attention_lpw<%s, 64, true, false>" % {"bf16": "__bf16", "fp16": "_Float16"}[dtype_name],
+        "kernel": "jc::time_attention_lpp<%s, true>" % {"bf16": "__bf16", "fp16": "_Float16"}[dtype_name],
         "launch_ms": round(ms, 5),
         "value": round(tf, 2),
         "unit": "TFLOP/s",
