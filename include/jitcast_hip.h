@@ -368,6 +368,30 @@ int jc_c2_assemble(jc_ctx *ctx, const float *emb, const float *reg, float *x, in
 int jc_c2_gather_future(jc_ctx *ctx, const float *y, float *dec, int rows, int fs, int n, int h, int d);
 
 /*
+ * The forecast's host ends on the device. jc_c2_prep = ModelLayout.of's cut and live mask
+ * (J/chronos2/ModelLayout.java:70-116) + ModelPrep.of (J/chronos2/ModelPrep.java:38-72, instanceNorm
+ * 80-101, scaled/asinh 104-114) from the raw rows: row i of the outputs is input row order[i]
+ * (order nullable: i), context [rows, ld_context] holds `steps` steps per row of which the last
+ * min(steps, context_length) are kept and NaN-padded on the left to nc = ceil(kept / patch) whole
+ * patches; future (nullable) [rows, ld_future] holds future_steps <= h*patch known steps. Writes
+ * tokens [rows*(nc+h), 3*patch] (time encoding, arcsinh-scaled value or 0, observed flag), loc and
+ * scale [rows], live [rows*(nc+nreg+h)] int32. Mean and std in double rounded to float, as the
+ * reference; only the order of the double sums may differ from its sequential loop.
+ */
+int jc_c2_prep(jc_ctx *ctx, const float *context, int64_t ld_context, int steps, const float *future,
+               int64_t ld_future, int future_steps, const int32_t *order, int rows, int context_length, int patch,
+               int h, int nreg, float time_scale, int arcsinh, float *tokens, float *loc, float *scale,
+               int32_t *live);
+
+/*
+ * ModelPrep.finish (J/chronos2/ModelPrep.java:117-143): out [order[i]][k][p*patch + s] =
+ * sinh(raw[(i*h + p)*q*patch + k*patch + s]) * scale[i] + loc[i] (without sinh when arcsinh is 0),
+ * rounded as the reference (float multiply, then float add). order nullable: i.
+ */
+int jc_c2_finish(jc_ctx *ctx, const float *raw, const float *loc, const float *scale, const int32_t *order, int rows,
+                 int h, int q, int patch, int arcsinh, float *out);
+
+/*
  * out [m, dout] = output(ReLU(hidden(x))) + residual(x): a Chronos-2 residual block (the input and
  * output patch embeddings), as Chronos2Forward.Plan.residual queues it
  * (J/chronos2/tornado/Chronos2Forward.java:306-311; CPU CpuChronos2.Residual.apply,

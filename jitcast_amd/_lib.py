@@ -35,7 +35,7 @@ class JitcastArgumentError(JitcastError, ValueError):
 
 
 _c = ctypes
-_vp, _i, _f, _sz = _c.c_void_p, _c.c_int, _c.c_float, _c.c_size_t
+_vp, _i, _f, _sz, _i64 = _c.c_void_p, _c.c_int, _c.c_float, _c.c_size_t, _c.c_int64
 _i32p = _c.c_void_p  # device int32 pointers are passed as addresses
 
 # name -> (restype, argtypes); every function the header declares must be listed here
@@ -81,6 +81,8 @@ SIGNATURES = {
     "jc_to_lp": (_i, [_vp, _vp, _vp, _c.c_int64, _i]),
     "jc_c2_assemble": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i]),
     "jc_c2_gather_future": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i]),
+    "jc_c2_prep": (_i, [_vp, _vp, _i64, _i, _vp, _i64, _i, _vp, _i, _i, _i, _i, _i, _f, _i, _vp, _vp, _vp, _vp]),
+    "jc_c2_finish": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
     "jc_c2_residual": (_i, [_vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp]),
     "jc_ts_block_layout": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _c.POINTER(_i), _c.POINTER(_i), _vp,
                                 _vp, _vp]),

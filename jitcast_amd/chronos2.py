@@ -202,3 +202,36 @@ def to_lp(src, dst) -> None:
     _f32(src, "src")
     ctx = context(src.device.index or 0)
     _lib.call("jc_to_lp", ctx.handle, _ptr(src), _ptr(dst), ctypes.c_int64(src.numel()), _dtype_code(dst))
+
+
+def prep(series, future, order, rows: int, context_length: int, patch: int, h: int, nreg: int,
+         time_scale: float, arcsinh: bool):
+    """ModelLayout.of's cut and live mask plus ModelPrep.of on the device (jc_c2_prep): series
+    [rows, T] fp32 on the GPU (NaN where missing), future [rows, <= h*patch] or None, order int32
+    [rows] or None (output row i is input row order[i]). Returns (tokens [rows*(nc+h), 3*patch],
+    loc [rows], scale [rows], live [rows*(nc+nreg+h)] int32, nc), all on the series' device."""
+    import torch
+
+    ctx = context(series.device.index or 0)
+    t = int(series.shape[1])
+    kept = min(t, context_length)
+    nc = (kept + patch - 1) // patch
+    dev = series.device
+    tok = torch.empty(rows * (nc + h), 3 * patch, dtype=torch.float32, device=dev)
+    loc = torch.empty(rows, dtype=torch.float32, device=dev)
+    scale = torch.empty(rows, dtype=torch.float32, device=dev)
+    live = torch.empty(rows * (nc + nreg + h), dtype=torch.int32, device=dev)
+    fs = int(future.shape[1]) if future is not None else 0
+    ldf = int(future.stride(0)) if future is not None else 0
+    _lib.call("jc_c2_prep", ctx.handle, _ptr(series), ctypes.c_int64(series.stride(0)), t, _ptr(future),
+              ctypes.c_int64(ldf), fs, _ptr(order), rows, context_length, patch, h, nreg, ctypes.c_float(time_scale),
+              int(bool(arcsinh)), _ptr(tok), _ptr(loc), _ptr(scale), _ptr(live))
+    return tok, loc, scale, live, nc
+
+
+def finish(raw, loc, scale, order, rows: int, h: int, q: int, patch: int, arcsinh: bool, out) -> None:
+    """ModelPrep.finish on the device (jc_c2_finish): out [rows, q, h*patch] (row order[i] of out
+    from row i of raw [rows*h, q*patch]) = sinh(raw) * scale + loc."""
+    ctx = context(raw.device.index or 0)
+    _lib.call("jc_c2_finish", ctx.handle, _ptr(raw), _ptr(loc), _ptr(scale), _ptr(order), rows, h, q, patch,
+              int(bool(arcsinh)), _ptr(out))

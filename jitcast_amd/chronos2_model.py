@@ -262,23 +262,43 @@ class HipChronos2Model:
     def forecast(self, context, group, future_covariates=None, h: int = 1) -> np.ndarray:
         """Quantile forecasts [rows, Q, h*P] for the input rows (group ids per row; rows of a group
         need not be adjacent: they are ordered as Chronos2Forward.groupOrder orders them and the
-        results are put back in input order)."""
+        results are put back in input order). The host ends run on the device too (jc_c2_prep,
+        jc_c2_finish): only the raw rows go up and the finished quantiles come down."""
         import torch
 
         c = self.c
-        lay = layout(c, context, group, future_covariates, h)
-        order = chronos2.group_order(lay.group)
-        if order is not None:
-            lay = Layout(lay.rows, lay.nc, lay.nreg, lay.h, lay.window[order], lay.future[order], lay.live[order],
-                         lay.group[order])
-        tok, loc, scale = prep(c, lay)
-        gs, ge = chronos2.group_bounds(lay.group)
+        ctx, group, fut = _check_inputs(c, context, group, future_covariates, h)
+        rows = ctx.shape[0]
+        order = chronos2.group_order(group)
+        gs, ge = chronos2.group_bounds(group[order] if order is not None else group)
         dev = self.dev
-        raw = self.forward_raw(torch.from_numpy(tok).to(dev), torch.from_numpy(lay.live.reshape(-1)).to(dev),
-                               torch.from_numpy(gs).to(dev), torch.from_numpy(ge).to(dev), lay.rows, lay.nc, lay.h)
-        out = finish(c, lay, raw.cpu().numpy(), loc, scale)
-        if order is not None:
-            back = np.empty_like(out)
-            back[order] = out
-            out = back
-        return out
+        up = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+        ord_t = up(order) if order is not None else None
+        nreg = 1 if c.use_reg_token else 0
+        tok, loc, scale, live, nc = chronos2.prep(up(ctx), up(fut) if fut is not None else None, ord_t, rows,
+                                                  c.context_length, c.patch_size, h, nreg, c.time_encoding_scale,
+                                                  c.use_arcsinh)
+        raw = self.forward_raw(tok, live, up(gs), up(ge), rows, nc, h)
+        out = torch.empty(rows, c.num_quantiles, h * c.patch_size, dtype=torch.float32, device=dev)
+        chronos2.finish(raw, loc, scale, ord_t, rows, h, c.num_quantiles, c.patch_size, c.use_arcsinh, out)
+        return out.cpu().numpy()
+
+
+def _check_inputs(c: Chronos2Config, context, group, future_covariates, h: int):
+    """The argument checks of ModelLayout.of (J/chronos2/ModelLayout.java:70-116): at least one
+    output patch, one group id per row, no more known future steps than h patches hold."""
+    if h < 1:
+        raise _lib.JitcastArgumentError(_lib.JC_EINVAL, f"output patches must be >= 1, got {h}")
+    ctx = np.asarray(context, np.float32)
+    if ctx.ndim != 2:
+        raise _lib.JitcastArgumentError(_lib.JC_EINVAL, "context must be [rows, steps]")
+    group = np.ascontiguousarray(np.asarray(group, np.int32))
+    if group.shape != (ctx.shape[0],):
+        raise _lib.JitcastArgumentError(_lib.JC_EINVAL, "group ids must have one entry per row")
+    fut = None
+    if future_covariates is not None:
+        fut = np.asarray(future_covariates, np.float32)
+        if fut.ndim != 2 or fut.shape[0] != ctx.shape[0] or fut.shape[1] > h * c.patch_size:
+            raise _lib.JitcastArgumentError(_lib.JC_EINVAL,
+                                            f"{h} output patches cannot hold {fut.shape[-1]} future steps")
+    return ctx, group, fut

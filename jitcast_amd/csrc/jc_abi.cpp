@@ -812,6 +812,43 @@ int jc_c2_assemble(jc_ctx* ctx, const float* emb, const float* reg, float* x, in
     return e == hipSuccess ? JC_OK : hip_fail(W, e);
 }
 
+int jc_c2_prep(jc_ctx* ctx, const float* context, int64_t ld_context, int steps, const float* future,
+               int64_t ld_future, int future_steps, const int32_t* order, int rows, int context_length, int patch,
+               int h, int nreg, float time_scale, int arcsinh, float* tokens, float* loc, float* scale,
+               int32_t* live) {
+    const char* W = "jc_c2_prep";
+    int rc = use(ctx, W);
+    if (rc) return rc;
+    if (rows < 0 || steps < 0 || context_length < 1 || patch < 1 || h < 1 || nreg < 0 || nreg > 1)
+        return fail(JC_EINVAL, "%s: sizes (rows=%d steps=%d context_length=%d patch=%d h=%d nreg=%d)", W, rows, steps,
+                    context_length, patch, h, nreg);
+    if (ld_context < steps || (future && (future_steps < 0 || future_steps > h * patch || ld_future < future_steps)))
+        return fail(JC_EINVAL, "%s: row strides (ld_context=%lld steps=%d ld_future=%lld future_steps=%d, h*patch=%d)",
+                    W, (long long)ld_context, steps, (long long)ld_future, future_steps, h * patch);
+    if (!(time_scale > 0.f)) return fail(JC_EINVAL, "%s: time_scale must be positive", W);
+    if (rows == 0) return JC_OK;
+    if ((!context && steps > 0) || !tokens || !loc || !scale || !live) return fail(JC_EINVAL, "%s: null buffer", W);
+    const int kept = steps < context_length ? steps : context_length;
+    const int nc = (kept + patch - 1) / patch;
+    hipError_t e = jc::c2_prep_launch(context, ld_context, steps, future, ld_future, future ? future_steps : 0, order,
+                                      rows, kept, nc, h, patch, nreg, time_scale, arcsinh, tokens, loc, scale, live,
+                                      ctx->stream);
+    return e == hipSuccess ? JC_OK : hip_fail(W, e);
+}
+
+int jc_c2_finish(jc_ctx* ctx, const float* raw, const float* loc, const float* scale, const int32_t* order, int rows,
+                 int h, int q, int patch, int arcsinh, float* out) {
+    const char* W = "jc_c2_finish";
+    int rc = use(ctx, W);
+    if (rc) return rc;
+    if (rows < 0 || h < 1 || q < 1 || patch < 1)
+        return fail(JC_EINVAL, "%s: sizes (rows=%d h=%d q=%d patch=%d)", W, rows, h, q, patch);
+    if (rows == 0) return JC_OK;
+    if (!raw || !loc || !scale || !out) return fail(JC_EINVAL, "%s: null buffer", W);
+    hipError_t e = jc::c2_finish_launch(raw, loc, scale, order, rows, h, q, patch, arcsinh, out, ctx->stream);
+    return e == hipSuccess ? JC_OK : hip_fail(W, e);
+}
+
 int jc_c2_gather_future(jc_ctx* ctx, const float* y, float* dec, int rows, int fs, int n, int h, int d) {
     const char* W = "jc_c2_gather_future";
     int rc = use(ctx, W);

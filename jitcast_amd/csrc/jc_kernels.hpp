@@ -86,4 +86,13 @@ hipError_t assemble_tokens_launch(const float* emb, const float* reg, float* x, 
                                   hipStream_t stream);
 hipError_t gather_future_launch(const float* y, float* dec, int rows, int fs, int n, int h, int d, hipStream_t stream);
 
+// The Chronos-2 host ends (c2_prep.hip): ModelLayout's cut and live mask plus ModelPrep.of from the
+// raw context rows; ModelPrep.finish into [rows][Q][h*P]. order (nullable) gathers input rows /
+// scatters output rows.
+hipError_t c2_prep_launch(const float* ctx, int64_t ld_ctx, int steps, const float* fut, int64_t ld_fut, int fut_steps,
+                          const int32_t* order, int rows, int kept, int nc, int h, int patch, int nreg, float time_scale,
+                          int arcsinh, float* tok, float* loc, float* scale, int32_t* live, hipStream_t stream);
+hipError_t c2_finish_launch(const float* raw, const float* loc, const float* scale, const int32_t* order, int rows,
+                            int h, int q, int patch, int arcsinh, float* out, hipStream_t stream);
+
 }  // namespace jc
