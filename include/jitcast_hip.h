@@ -338,7 +338,7 @@ int jc_c2_layer(jc_ctx *ctx, float *x, const jc_c2_layer_weights *w, const int32
  * (JC_GEMM_ACCUMULATE adds into C). c_dtype = dtype: C in the storage type, saturated to its finite
  * range (the reference's FP16 twins, Kernels.java:42-46), no ACCUMULATE. Replaces Kernels.gemmHalf
  * and the GemmEx FP16->FP32 path (J/tornado/Kernels.java:115-232; Chronos2Forward.java:377-409).
- *   k a multiple of 8, lda >= k and a multiple of 8, ldc >= n; a and w 16-byte aligned.
+ *   k a multiple of 8, lda >= k and a multiple of 8, lda < 2^22, ldc >= n; a and w 16-byte aligned.
  */
 int jc_linear_lp(jc_ctx *ctx, const void *a, int lda, const void *w, const float *bias, void *c, int ldc, int m,
                  int n, int k, int flags, int dtype, int c_dtype);

@@ -699,6 +699,7 @@ static int launch_linear_lp(jc_ctx* ctx, const char* W, const void* a, int lda, 
     if (k % 8 || k == 0) return fail(JC_EINVAL, "%s: k must be a positive multiple of 8 (got %d)", W, k);
     if (lda < k || lda % 8) return fail(JC_EINVAL, "%s: lda must be >= k and a multiple of 8 (got %d)", W, lda);
     if (ldc < n) return fail(JC_EINVAL, "%s: ldc must be >= n (got %d)", W, ldc);
+    if (lda >= (1 << 22)) return fail(JC_EINVAL, "%s: lda and k must be below 4194304 (got %d)", W, lda);
     if (!aligned16(a) || !aligned16(w)) return fail(JC_EINVAL, "%s: a and w must be 16-byte aligned", W);
     if (flags & ~(JC_GEMM_BIAS | JC_GEMM_ACCUMULATE | JC_GEMM_SILU | JC_GEMM_RELU))
         return fail(JC_EINVAL, "%s: unknown flags 0x%x", W, flags);
@@ -706,7 +707,7 @@ static int launch_linear_lp(jc_ctx* ctx, const char* W, const void* a, int lda, 
     if (c_dtype != JC_F32 && (flags & JC_GEMM_ACCUMULATE))
         return fail(JC_EINVAL, "%s: JC_GEMM_ACCUMULATE needs an fp32 C", W);
     jc::GemmLpArgs g{a, w, bias, c, m, n, k, lda, ldc, flags};
-    hipError_t e = jc::gemm_lp_launch(g, dtype == JC_F16, c_dtype != JC_F32, ctx->stream);
+    hipError_t e = jc::gemm_lp_launch(g, dtype == JC_F16, c_dtype != JC_F32, ctx->cus, ctx->stream);
     return e == hipSuccess ? JC_OK : hip_fail(W, e);
 }
 

@@ -73,7 +73,9 @@ struct GemmLpArgs {
     void* c;
     int m, n, k, lda, ldc, flags;
 };
-hipError_t gemm_lp_launch(const GemmLpArgs& g, bool fp16, bool out_lp, hipStream_t stream);
+// persistent: at most `cus` workgroups; m, n < 2^31 tiles; lda and k below 2^22 (a 256-row block of
+// either operand spans less than 2^31 bytes)
+hipError_t gemm_lp_launch(const GemmLpArgs& g, bool fp16, bool out_lp, int cus, hipStream_t stream);
 // y (storage type) = x * (1 / sqrt(mean(x^2) + eps)) * w per row of d (d a multiple of 4)
 hipError_t rms_norm_lp_launch(const float* x, void* y, const float* w, int rows, int d, float eps, bool fp16,
                               hipStream_t stream);

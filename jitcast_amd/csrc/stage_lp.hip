@@ -10,12 +10,18 @@
 // Storage-type outputs saturate to the type's finite range, as the reference's FP16 twins do
 // (Kernels.java:42-46).
 //
-// Tiling (measured best of 128/256 x 128/256 x 32/64 on the layer's shapes): a 1024-thread
-// workgroup owns a 256x256 tile of C; wave w owns the 64x64 block (w / 4, w % 4) as 2x2 MFMA tiles
-// of 32x32. K advances 64 at a time through double-buffered LDS (A and W tiles of 256 rows x 64
-// elements, rows padded to 72 elements so that 16-byte reads of consecutive rows hit distinct
-// banks); the next stage's loads are in flight in registers during the current stage's 32 MFMAs
-// per wave. MFMA layouts (32x32x16): A lane i+32g = A[i][8g..8g+7], B lane j+32g = B[8g..8g+7][j],
+// Tiling: a 512-thread workgroup owns a 256x256 tile of C; wave w owns the 128x64 block
+// (w / 4, w % 4) as 4x2 MFMA tiles of 32x32 (128 accumulators per lane), which reads 6 KB of
+// operands from LDS per 8 MFMAs. K advances 64 at a time through two LDS stages (A and W tiles of
+// 256 rows x 64 elements, 128 KB in all). The tiles arrive by direct-to-LDS buffer loads
+// (buffer_load_dwordx4 ... lds, 1 KB per wave instruction): a row of 64 elements is 8 chunks of
+// 16 bytes, and chunk c of row r sits at position c ^ (r & 7), so the MFMA operand reads (16 bytes
+// of 32 consecutive rows) hit distinct banks. Out-of-range rows and k columns read as zero through
+// the buffer descriptor's range check, so any m, n and k (a multiple of 8) need no clamping.
+// The grid is persistent (one workgroup per CU): a workgroup walks its tiles, and the first stage
+// of its next tile loads while the epilogue of the current one stores. Tiles that share a row
+// block of A run at the same time on one XCD, so A is read from HBM about once.
+// MFMA layouts (32x32x16): A lane i+32g = A[i][8g..8g+7], B lane j+32g = B[8g..8g+7][j],
 // D lane j+32g reg r = D[8(r/4) + 4g + r%4][j].
 #include "jc_common.hpp"
 #include "jc_kernels.hpp"
@@ -27,16 +33,53 @@ namespace {
 using namespace lp;
 
 constexpr int kBM = 256, kBN = 256, kBK = 64;
-constexpr int kPitch = kBK + 8;  // elements per staged row
-constexpr int kWM = 4, kWN = 4;  // waves along M and N
+constexpr int kWM = 2, kWN = 4;  // waves along M and N
 constexpr int kThreads = kWM * kWN * kWave;
-constexpr int kPieces = kBM * kBK / 8 / kThreads;  // 16-byte pieces per thread and operand
+constexpr int kWaves = kWM * kWN;
+constexpr int kTM = kBM / kWM / 32, kTN = kBN / kWN / 32;  // 32x32 tiles per wave: 4 x 2
+static_assert(kTN * 32 == 64 && kWaves / 2 * 2048 * 4 == kBM * kBK * 2, "epilogue staging: 32 x 64 floats per wave");
+constexpr int kLoads = kBM * kBK * 2 / 1024 / (kWM * kWN);  // 1 KB loads per wave, operand and stage: 4
+constexpr uint32_t kOob = 0x80000000u;                      // a buffer offset past every range: reads 0
 
-template <typename T>
-struct LpTile {
-    uint16_t a[2][kBM * kPitch];
-    uint16_t w[2][kBN * kPitch];
+struct alignas(16) LpTile {  // 16-byte aligned, so operand reads stay ds_read_b128
+    uint16_t a[2][kBM * kBK];
+    uint16_t w[2][kBN * kBK];
+    float bias[2][kBN];  // the bias of the tile in flight, by tile parity
 };
+
+// element offset of chunk c (8 elements) of row r in a swizzled stage
+__device__ __forceinline__ int gswz(int r, int c) { return r * kBK + ((c ^ (r & 7)) << 3); }
+
+// raw buffer descriptor of `bytes` bytes at p (the base fits 48 bits, stride 0)
+__device__ __forceinline__ u32x4 buf_desc(const void* p, uint32_t bytes) {
+    const uint64_t a = (uint64_t)p;
+    return u32x4{(uint32_t)a, (uint32_t)(a >> 32) & 0xFFFFu, bytes, kRsrcWord3};
+}
+
+// 16 bytes per lane from rsrc + voff into LDS at lds + 16 * lane (zero when out of range)
+__device__ __forceinline__ void dma16(u32x4 rsrc, uint32_t voff, const void* lds) {
+    const uint32_t m0 = (uint32_t)(size_t)(__attribute__((address_space(3))) const void*)lds;
+    asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rsrc), "s"(m0)
+                 : "memory", "m0");
+}
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+// a copy of x the compiler cannot see through (values derived from it are not hoisted)
+__device__ __forceinline__ int opaque(int x) {
+    asm volatile("" : "+v"(x));
+    return x;
+}
+// 4 bytes per lane from rsrc + voff into LDS at lds + 4 * lane (zero when out of range)
+__device__ __forceinline__ void dma4(u32x4 rsrc, uint32_t voff, const void* lds) {
+    const uint32_t m0 = (uint32_t)(size_t)(__attribute__((address_space(3))) const void*)lds;
+    asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dword %0, %1, 0 offen lds" ::"v"(voff), "s"(rsrc), "s"(m0)
+                 : "memory", "m0");
+}
+// this wave's LDS accesses done, then the workgroup barrier
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // clamp to the storage type's finite range, keeping NaN (TornadoMath.clamp propagates it)
 __device__ __forceinline__ float clamp_finite(float v, float m) { return v != v ? v : fminf(fmaxf(v, -m), m); }
@@ -47,95 +90,244 @@ __device__ __forceinline__ T saturate(float v) {
 }
 
 template <typename T, bool OUT_LP>
-__global__ __launch_bounds__(kThreads, 1) void gemm_lp(const GemmLpArgs g) {
+__global__ __launch_bounds__(kThreads, 1) void gemm_lp(const GemmLpArgs g, uint32_t tiles_n, uint32_t total, int vec) {
     typedef typename Lp<T>::x8 x8;
-    __shared__ LpTile<T> lds;
+    __shared__ LpTile lds;
     const T* __restrict__ A = static_cast<const T*>(g.a);
     const T* __restrict__ W = static_cast<const T*>(g.w);
-    const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+    const int lane = threadIdx.x % kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int j = lane % 32, hg = lane / 32;
-    const uint32_t nbn = (g.n + kBN - 1) / kBN;
-    const uint32_t total = nbn * ((g.m + kBM - 1) / kBM);
-    const uint32_t logical = xcd_remap(blockIdx.x, total);
-    const int m0 = (logical / nbn) * kBM, n0 = (logical % nbn) * kBN;
     const int wm = wave / kWN, wn = wave % kWN;
-
-    // staging: 2048 pieces per operand tile (row p / 8, k 8(p % 8)); k past g.k reads as zero
-    u32x4 ra[kPieces], rw[kPieces];
-    auto load = [&](int k0) {
-#pragma unroll
-        for (int u = 0; u < kPieces; u++) {
-            const int p = tid + u * kThreads, r = p / (kBK / 8), kc = k0 + 8 * (p % (kBK / 8));
-            const int ar = m0 + r, wr = n0 + r;
-            ra[u] = ar < g.m && kc < g.k ? *reinterpret_cast<const u32x4*>(A + (size_t)ar * g.lda + kc) : u32x4{0u, 0u, 0u, 0u};
-            rw[u] = wr < g.n && kc < g.k ? *reinterpret_cast<const u32x4*>(W + (size_t)wr * g.k + kc) : u32x4{0u, 0u, 0u, 0u};
-        }
-    };
-    auto store = [&](int buf) {
-#pragma unroll
-        for (int u = 0; u < kPieces; u++) {
-            const int p = tid + u * kThreads, r = p / (kBK / 8), kc = 8 * (p % (kBK / 8));
-            *reinterpret_cast<u32x4*>(&lds.a[buf][r * kPitch + kc]) = ra[u];
-            *reinterpret_cast<u32x4*>(&lds.w[buf][r * kPitch + kc]) = rw[u];
-        }
-    };
-
-    floatx16 acc[2][2];
-#pragma unroll
-    for (int ti = 0; ti < 2; ti++)
-#pragma unroll
-        for (int tj = 0; tj < 2; tj++) acc[ti][tj] = floatx16{0};
-
     const int stages = (g.k + kBK - 1) / kBK;
-    load(0);
-    store(0);
-    __syncthreads();
-    for (int st = 0; st < stages; st++) {
-        const int buf = st & 1;
-        if (st + 1 < stages) load((st + 1) * kBK);
-#pragma unroll
-        for (int kk = 0; kk < kBK / 16; kk++) {
-            x8 av[2], wv[2];
-#pragma unroll
-            for (int t = 0; t < 2; t++) {
-                av[t] = __builtin_bit_cast(x8, *reinterpret_cast<const u32x4*>(&lds.a[buf][(64 * wm + 32 * t + j) * kPitch + 16 * kk + 8 * hg]));
-                wv[t] = __builtin_bit_cast(x8, *reinterpret_cast<const u32x4*>(&lds.w[buf][(64 * wn + 32 * t + j) * kPitch + 16 * kk + 8 * hg]));
-            }
-#pragma unroll
-            for (int ti = 0; ti < 2; ti++)
-#pragma unroll
-                for (int tj = 0; tj < 2; tj++) acc[ti][tj] = Lp<T>::mfma(av[ti], wv[tj], acc[ti][tj]);
-        }
-        if (st + 1 < stages) store(buf ^ 1);
-        __syncthreads();
-    }
+    // staging: load u of this wave fills rows 8(kLoads * wave + u) .. +7; lane -> row lane / 8,
+    // position lane % 8, which holds chunk (lane % 8) ^ (lane / 8)
+    const uint32_t a_row = (uint32_t)g.lda * 2u, w_row = (uint32_t)g.k * 2u;
 
-    // epilogue: reg r of lane (j, hg) in tile (ti, tj) is C[row 8(r/4) + 4hg + r%4][col j]; bias,
-    // activation, accumulate, in Kernels.gemm's order
+    // loads u0 .. u1 - 1 of stage st of a tile into stage buffer buf; with stage 0 and u0 = 0, the
+    // tile's bias into bias slot bslot
+    auto issue = [&](uint32_t tile, int st, int buf, int bslot, int u0, int u1) __attribute__((always_inline)) {
+        const int m0 = (int)(tile / tiles_n) * kBM, n0 = (int)(tile % tiles_n) * kBN;
+        if (st == 0 && u0 == 0 && wave == 0 && (g.flags & kGemmBias)) {
+            const u32x4 rb = buf_desc(g.bias + n0, (uint32_t)min(kBN, g.n - n0) * 4u);
 #pragma unroll
-    for (int ti = 0; ti < 2; ti++)
+            for (int u = 0; u < kBN / kWave; u++) dma4(rb, 4u * (uint32_t)(kWave * u + opaque(lane)), &lds.bias[bslot][kWave * u]);
+        }
+        const u32x4 ra = buf_desc(A + (size_t)m0 * g.lda, (uint32_t)min(kBM, g.m - m0) * a_row);
+        const u32x4 rw = buf_desc(W + (size_t)n0 * g.k, (uint32_t)min(kBN, g.n - n0) * w_row);
+        // recomputed per call from an opaque lane id, not hoisted into long-lived registers
+        const int ln = opaque(lane), srow = ln / 8, schunk = (ln % 8) ^ srow;
+        const int kc = st * kBK + 8 * schunk;
+        const bool kin = kc < g.k;
 #pragma unroll
-        for (int tj = 0; tj < 2; tj++) {
-            const int col = n0 + 64 * wn + 32 * tj + j;
-            if (col >= g.n) continue;
-            const float b = (g.flags & kGemmBias) ? g.bias[col] : 0.f;
+        for (int u = u0; u < u1; u++) {
+            const uint32_t r = 8 * (kLoads * wave + u) + srow;
+            dma16(ra, kin ? r * a_row + 2u * kc : kOob, &lds.a[buf][8 * (kLoads * wave + u) * kBK]);
+            dma16(rw, kin ? r * w_row + 2u * kc : kOob, &lds.w[buf][8 * (kLoads * wave + u) * kBK]);
+        }
+    };
+
+    // persistent walk: round i takes tiles i * gridDim.x + (this workgroup's slot in XCD order)
+    const uint32_t slot = xcd_remap(blockIdx.x, gridDim.x);
+    uint32_t tile = slot;
+    if (tile >= total) return;
+    issue(tile, 0, 0, 0, 0, kLoads);
+    // VMEM instructions the previous tile's epilogue issued after this tile's first-stage loads
+    // (whole tiles only; 0 = wait for everything). Vector memory operations retire in issue order,
+    // so waiting until at most that many are outstanding waits for the loads and leaves the
+    // epilogue's stores draining behind the next MFMAs.
+    int younger = 0;
+    const bool accumulate = !OUT_LP && (g.flags & kGemmAccumulate);
+    for (int it = 0;; it++) {
+        const int m0 = (int)(tile / tiles_n) * kBM, n0 = (int)(tile % tiles_n) * kBN;
+        const int er = lane / 16, ec = 4 * (lane % 16);
+        const int col0 = n0 + 64 * wn + ec;  // this lane's 4 output columns in the epilogue
+        floatx16 acc[kTM][kTN];
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int row = m0 + 64 * wm + 32 * ti + 8 * (r / 4) + 4 * hg + r % 4;
-                if (row >= g.m) continue;
-                float v = acc[ti][tj][r] + b;
-                if (g.flags & kGemmSilu) v = v / (1.f + __expf(-v));
-                if (g.flags & kGemmRelu) v = (v > 0.f || v != v) ? v : 0.f;
-                const size_t ci = (size_t)row * g.ldc + col;
-                if (OUT_LP) {
-                    static_cast<T*>(g.c)[ci] = saturate<T>(v);
-                } else {
-                    float* c = static_cast<float*>(g.c);
-                    if (g.flags & kGemmAccumulate) v += c[ci];
-                    c[ci] = v;
-                }
+        for (int ti = 0; ti < kTM; ti++)
+#pragma unroll
+            for (int tj = 0; tj < kTN; tj++) acc[ti][tj] = floatx16{0};
+
+        for (int st = 0; st < stages; st++) {
+            const int buf = st & 1;
+            // stage st has landed everywhere, and every wave is done with stage st - 1's buffer
+            if (st == 0 && younger == 63) {
+                wait_vm<63>();
+            } else if (st == 0 && younger == 32) {
+                wait_vm<32>();
+            } else {
+                wait_vm<0>();
+            }
+            lds_barrier();
+            // the next stage's loads are spread over the first two k-steps, so the per-CU address
+            // unit works through them while the MFMAs run instead of stalling every wave at once
+#pragma unroll
+            for (int kk = 0; kk < kBK / 16; kk++) {
+                if (kk < 2 && st + 1 < stages) issue(tile, st + 1, buf ^ 1, 0, kk * kLoads / 2, (kk + 1) * kLoads / 2);
+                const int c = 2 * kk + hg;
+                x8 av[kTM], wv[kTN];
+#pragma unroll
+                for (int ti = 0; ti < kTM; ti++)
+                    av[ti] = __builtin_bit_cast(x8, *reinterpret_cast<const u32x4*>(&lds.a[buf][gswz(128 * wm + 32 * ti + j, c)]));
+#pragma unroll
+                for (int tj = 0; tj < kTN; tj++)
+                    wv[tj] = __builtin_bit_cast(x8, *reinterpret_cast<const u32x4*>(&lds.w[buf][gswz(64 * wn + 32 * tj + j, c)]));
+#pragma unroll
+                for (int ti = 0; ti < kTM; ti++)
+#pragma unroll
+                    for (int tj = 0; tj < kTN; tj++) acc[ti][tj] = Lp<T>::mfma(av[ti], wv[tj], acc[ti][tj]);
             }
         }
+        // every wave is done with both stages: the next tile's first stage may load
+        const uint32_t next = tile + gridDim.x;
+        wait_vm<0>();
+        lds_barrier();
+        if (next < total) issue(next, 0, 0, (it + 1) & 1, 0, kLoads);
+
+        // epilogue, 32 rows of the wave's block at a time through the wave's 8 KB of the stage the
+        // next tile does not load into: the MFMA layout in (reg r of lane (j, hg) in tile (ti, tj)
+        // is row 8(r/4) + 4hg + r%4, column 32tj + j of the block), rows of 4 consecutive columns
+        // out, so each lane stores 16 bytes (fp32) or 8 bytes (storage type) of one row. Bias,
+        // activation, accumulate, in Kernels.gemm's order.
+        float* ep = reinterpret_cast<float*>(wave < kWaves / 2 ? lds.a[1] : lds.w[1]) + (wave % (kWaves / 2)) * 2048;
+        // the bias came with the tile's first stage (zero past n)
+        const floatx4 b4 = (g.flags & kGemmBias) ? *reinterpret_cast<const floatx4*>(&lds.bias[it & 1][64 * wn + ec])
+                                                 : floatx4{0.f, 0.f, 0.f, 0.f};
+        // block ti through LDS: write it, then read back rows vv[q - q0] = row 4q + lane / 16,
+        // columns 4 (lane % 16) .. + 3 for q in [q0, q0 + nq) (the reads issued before any use)
+        auto to_lds = [&](int ti) __attribute__((always_inline)) {
+#pragma unroll
+            for (int tj = 0; tj < kTN; tj++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int R = 8 * (r / 4) + 4 * hg + r % 4;
+                    ep[R * 64 + ((32 * tj + j) ^ ((R & 4) << 3))] = acc[ti][tj][r];
+                }
+            __builtin_amdgcn_wave_barrier();
+            asm volatile("" ::: "memory");
+        };
+        auto rows = [&](int q0, int nq, floatx4* vv) __attribute__((always_inline)) {
+#pragma unroll
+            for (int q = q0; q < q0 + nq; q++) {
+                const int R = 4 * q + er;
+                vv[q - q0] = *reinterpret_cast<const floatx4*>(&ep[R * 64 + (ec ^ ((R & 4) << 3))]);
+            }
+        };
+        auto to_rows = [&](int ti, floatx4* vv) __attribute__((always_inline)) {
+            to_lds(ti);
+            rows(0, 8, vv);
+        };
+        auto finish = [&](floatx4 v) __attribute__((always_inline)) {
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                v[u] += b4[u];
+                if (g.flags & kGemmSilu) v[u] = v[u] / (1.f + __expf(-v[u]));
+                if (g.flags & kGemmRelu) v[u] = (v[u] > 0.f || v[u] != v[u]) ? v[u] : 0.f;
+            }
+            return v;
+        };
+        const int row0 = m0 + 128 * wm + er;  // + 32 ti + 4 q
+        const bool whole = vec && m0 + kBM <= g.m && n0 + kBN <= g.n;
+        if (whole) {
+            // every access in range: one 16- or 8-byte buffer store (and load) per lane and 4 rows,
+            // the rows' offsets in the scalar operand, no branches, so the instruction count below
+            // is exact
+            constexpr uint32_t kElt = OUT_LP ? 2u : 4u;
+            const __amdgpu_buffer_rsrc_t rc =
+                make_rsrc(static_cast<char*>(g.c) + (size_t)m0 * g.ldc * kElt, (uint32_t)kBM * g.ldc * kElt);
+            const uint32_t voff0 = ((uint32_t)(128 * wm + er) * g.ldc + (uint32_t)col0) * kElt;
+            const uint32_t rows4 = 4u * g.ldc * kElt;
+            // row 4q of the block in the vector offset, block ti in the scalar one
+            auto voffq = [&](int q) __attribute__((always_inline)) { return voff0 + (uint32_t)q * rows4; };
+            auto soffb = [&](int ti) __attribute__((always_inline)) { return (uint32_t)ti * 8u * rows4; };
+            if (accumulate) {
+                u32x4 cv[2][8];
+#pragma unroll
+                for (int q = 0; q < 8; q++) cv[0][q] = __builtin_amdgcn_raw_buffer_load_b128(rc, voffq(q), soffb(0), 0);
+#pragma unroll
+                for (int ti = 0; ti < kTM; ti++) {
+                    to_lds(ti);  // frees acc[ti] before the next block's loads take registers
+                    if (ti + 1 < kTM) {
+#pragma unroll
+                        for (int q = 0; q < 8; q++)
+                            cv[(ti + 1) & 1][q] = __builtin_amdgcn_raw_buffer_load_b128(rc, voffq(q), soffb(ti + 1), 0);
+                    }
+#pragma unroll
+                    for (int h = 0; h < 2; h++) {
+                        floatx4 vv[4];
+                        rows(4 * h, 4, vv);
+#pragma unroll
+                        for (int q = 4 * h; q < 4 * h + 4; q++) {
+                            const floatx4 v = finish(vv[q - 4 * h]) + __builtin_bit_cast(floatx4, cv[ti & 1][q]);
+                            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rc, voffq(q), soffb(ti), 0);
+                        }
+                    }
+                    asm volatile("" ::: "memory");
+                }
+                younger = 63;  // 32 loads and 32 stores (the wait is capped at 63)
+            } else {
+#pragma unroll
+                for (int ti = 0; ti < kTM; ti++) {
+                    floatx4 vv[8];
+                    to_rows(ti, vv);
+#pragma unroll
+                    for (int q = 0; q < 8; q++) {
+                        const floatx4 v = finish(vv[q]);
+                        if (OUT_LP) {
+                            floatx4 sv;
+#pragma unroll
+                            for (int u = 0; u < 4; u++) sv[u] = clamp_finite(v[u], Enc<T>::kMax);
+                            __builtin_amdgcn_raw_buffer_store_b64(narrow4<T>(sv), rc, voffq(q), soffb(ti), 0);
+                        } else {
+                            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rc, voffq(q), soffb(ti), 0);
+                        }
+                    }
+                    asm volatile("" ::: "memory");
+                }
+                younger = 32;  // 32 stores
+            }
+        } else {
+#pragma unroll
+            for (int ti = 0; ti < kTM; ti++) {
+                floatx4 vv[8];
+                to_rows(ti, vv);
+#pragma unroll
+                for (int q = 0; q < 8; q++) {
+                    const floatx4 v = finish(vv[q]);
+                    const int row = row0 + 32 * ti + 4 * q;
+                    if (row >= g.m || col0 >= g.n) continue;
+                    const size_t ci = (size_t)row * g.ldc + col0;
+                    if (vec && col0 + 3 < g.n) {
+                        if (OUT_LP) {
+                            floatx4 sv;
+#pragma unroll
+                            for (int u = 0; u < 4; u++) sv[u] = clamp_finite(v[u], Enc<T>::kMax);
+                            *reinterpret_cast<u32x2*>(static_cast<T*>(g.c) + ci) = narrow4<T>(sv);
+                        } else {
+                            floatx4* cp = reinterpret_cast<floatx4*>(static_cast<float*>(g.c) + ci);
+                            *cp = accumulate ? v + *cp : v;
+                        }
+                    } else {
+#pragma unroll
+                        for (int u = 0; u < 4; u++) {
+                            if (col0 + u >= g.n) break;
+                            if (OUT_LP) {
+                                static_cast<T*>(g.c)[ci + u] = saturate<T>(v[u]);
+                            } else {
+                                float* cp = static_cast<float*>(g.c) + ci + u;
+                                *cp = accumulate ? v[u] + *cp : v[u];
+                            }
+                        }
+                    }
+                }
+                // this block's reads are issued before the next block's writes (LDS keeps a wave's order)
+                asm volatile("" ::: "memory");
+            }
+            younger = 0;
+        }
+        if (next >= total) break;
+        tile = next;
+    }
 }
 
 // y = twin(x * (1 / sqrt(mean(x^2) + eps)) * w), one wave per row, x fp32, y in the storage type
@@ -173,14 +365,20 @@ __global__ __launch_bounds__(256) void to_lp(const float* __restrict__ x, T* __r
 
 }  // namespace
 
-hipError_t gemm_lp_launch(const GemmLpArgs& g, bool fp16, bool out_lp, hipStream_t stream) {
-    const uint64_t grid = (uint64_t)((g.m + kBM - 1) / kBM) * ((g.n + kBN - 1) / kBN);
+hipError_t gemm_lp_launch(const GemmLpArgs& g, bool fp16, bool out_lp, int cus, hipStream_t stream) {
+    const uint64_t tiles_n = (uint64_t)((g.n + kBN - 1) / kBN);
+    const uint64_t total = (uint64_t)((g.m + kBM - 1) / kBM) * tiles_n;
+    const uint32_t grid = (uint32_t)(total < (uint64_t)cus ? total : (uint64_t)cus);
+    const uint32_t tn = (uint32_t)tiles_n, tt = (uint32_t)total;
+    // whole-quad stores need every row start aligned: 16 bytes (fp32 C) or 8 (storage-type C)
+    // (and a 256-row block of C addressable with 32-bit offsets)
+    const int vec = g.ldc % 4 == 0 && g.ldc < (1 << 22) && (size_t)g.c % (out_lp ? 8 : 16) == 0;
     if (fp16) {
-        if (out_lp) hipLaunchKernelGGL((gemm_lp<_Float16, true>), dim3((uint32_t)grid), dim3(kThreads), 0, stream, g);
-        else hipLaunchKernelGGL((gemm_lp<_Float16, false>), dim3((uint32_t)grid), dim3(kThreads), 0, stream, g);
+        if (out_lp) hipLaunchKernelGGL((gemm_lp<_Float16, true>), dim3(grid), dim3(kThreads), 0, stream, g, tn, tt, vec);
+        else hipLaunchKernelGGL((gemm_lp<_Float16, false>), dim3(grid), dim3(kThreads), 0, stream, g, tn, tt, vec);
     } else {
-        if (out_lp) hipLaunchKernelGGL((gemm_lp<__bf16, true>), dim3((uint32_t)grid), dim3(kThreads), 0, stream, g);
-        else hipLaunchKernelGGL((gemm_lp<__bf16, false>), dim3((uint32_t)grid), dim3(kThreads), 0, stream, g);
+        if (out_lp) hipLaunchKernelGGL((gemm_lp<__bf16, true>), dim3(grid), dim3(kThreads), 0, stream, g, tn, tt, vec);
+        else hipLaunchKernelGGL((gemm_lp<__bf16, false>), dim3(grid), dim3(kThreads), 0, stream, g, tn, tt, vec);
     }
     return hipGetLastError();
 }

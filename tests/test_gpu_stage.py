@@ -127,7 +127,8 @@ LP = {"bf16": torch.bfloat16, "fp16": torch.float16}
 
 
 @pytest.mark.parametrize("dt", sorted(LP))
-@pytest.mark.parametrize("m,n,k", [(1, 16, 16), (37, 100, 64), (300, 257, 776), (513, 256, 768)])
+@pytest.mark.parametrize("m,n,k", [(1, 16, 16), (37, 100, 64), (300, 257, 776), (513, 256, 768),
+                                   (20011, 1000, 72)])  # 316 tiles: several per workgroup
 @pytest.mark.parametrize("flags,bias,out", [(0, False, "lp"), (chronos2.GEMM_RELU, True, "lp"), (0, True, "f32"),
                                             (chronos2.GEMM_ACCUMULATE, False, "f32"),
                                             (chronos2.GEMM_RELU | chronos2.GEMM_ACCUMULATE, True, "f32")])
@@ -148,6 +149,25 @@ def test_linear_lp_matches_oracle(gpu, oracle, m, n, k, flags, bias, out, dt):
     got = c.float().cpu().numpy()
     tol = 1e-5 if out == "f32" else 2 ** -8  # one rounding to the storage type
     assert oracle.rel_max_error(got, exp) <= tol
+
+
+@pytest.mark.parametrize("dt", sorted(LP))
+def test_linear_lp_strided_operands(gpu, oracle, dt):
+    """A, W and C as row slices of wider buffers (lda = 96 > k = 40, ldc = 70 > n = 65)."""
+    r = np.random.default_rng(3)
+    m, n, k = 300, 65, 40
+    abuf = r.standard_normal((m, 96)).astype(np.float32)
+    w = (r.standard_normal((n, k)) / np.sqrt(k)).astype(np.float32)
+    cbuf = r.standard_normal((m, 70)).astype(np.float32)
+    at, wt = _t(abuf).to(LP[dt]), _t(w).to(LP[dt])
+    c = _t(cbuf)
+    chronos2.linear_lp(at, wt, c, flags=chronos2.GEMM_ACCUMULATE, m=m, n=n, k=k, lda=96, ldc=70)
+    torch.cuda.synchronize()
+    got = c.cpu().numpy()
+    exp = cbuf.copy()
+    exp[:, :n] += oracle.linear(np.ascontiguousarray(at.float().cpu().numpy()[:, :k]), wt.float().cpu().numpy())
+    assert oracle.rel_max_error(got[:, :n], exp[:, :n]) <= 1e-5
+    np.testing.assert_array_equal(got[:, n:], cbuf[:, n:])  # columns past n untouched
 
 
 @pytest.mark.parametrize("dt", sorted(LP))
