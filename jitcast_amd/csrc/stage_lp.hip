@@ -59,7 +59,7 @@ __device__ __forceinline__ u32x4 buf_desc(const void* p, uint32_t bytes) {
 // 16 bytes per lane from rsrc + voff into LDS at lds + 16 * lane (zero when out of range)
 __device__ __forceinline__ void dma16(u32x4 rsrc, uint32_t voff, const void* lds) {
     const uint32_t m0 = (uint32_t)(size_t)(__attribute__((address_space(3))) const void*)lds;
-    asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rsrc), "s"(m0)
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rsrc), "s"(m0)
                  : "memory", "m0");
 }
 template <int N>
@@ -75,7 +75,7 @@ __device__ __forceinline__ int opaque(int x) {
 // 4 bytes per lane from rsrc + voff into LDS at lds + 4 * lane (zero when out of range)
 __device__ __forceinline__ void dma4(u32x4 rsrc, uint32_t voff, const void* lds) {
     const uint32_t m0 = (uint32_t)(size_t)(__attribute__((address_space(3))) const void*)lds;
-    asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dword %0, %1, 0 offen lds" ::"v"(voff), "s"(rsrc), "s"(m0)
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dword %0, %1, 0 offen lds" ::"v"(voff), "s"(rsrc), "s"(m0)
                  : "memory", "m0");
 }
 // this wave's LDS accesses done, then the workgroup barrier
@@ -87,6 +87,18 @@ __device__ __forceinline__ float clamp_finite(float v, float m) { return v != v 
 template <typename T>
 __device__ __forceinline__ T saturate(float v) {
     return (T)clamp_finite(v, Enc<T>::kMax);
+}
+
+// bias, then the activation (0 none, 1 SiLU, 2 ReLU keeping NaN), in Kernels.gemm's order
+template <int ACT>
+__device__ __forceinline__ floatx4 activate(floatx4 v, floatx4 b) {
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        v[u] += b[u];
+        if (ACT == 1) v[u] = v[u] / (1.f + __expf(-v[u]));
+        if (ACT == 2) v[u] = (v[u] > 0.f || v[u] != v[u]) ? v[u] : 0.f;
+    }
+    return v;
 }
 
 template <typename T, bool OUT_LP>
@@ -228,38 +240,43 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_lp(const GemmLpArgs g, uint3
         };
         const int row0 = m0 + 128 * wm + er;  // + 32 ti + 4 q
         const bool whole = vec && m0 + kBM <= g.m && n0 + kBN <= g.n;
-        if (whole) {
-            // every access in range: one 16- or 8-byte buffer store (and load) per lane and 4 rows,
-            // the rows' offsets in the scalar operand, no branches, so the instruction count below
-            // is exact
-            constexpr uint32_t kElt = OUT_LP ? 2u : 4u;
-            const __amdgpu_buffer_rsrc_t rc =
-                make_rsrc(static_cast<char*>(g.c) + (size_t)m0 * g.ldc * kElt, (uint32_t)kBM * g.ldc * kElt);
-            const uint32_t voff0 = ((uint32_t)(128 * wm + er) * g.ldc + (uint32_t)col0) * kElt;
-            const uint32_t rows4 = 4u * g.ldc * kElt;
-            // row 4q of the block in the vector offset, block ti in the scalar one
-            auto voffq = [&](int q) __attribute__((always_inline)) { return voff0 + (uint32_t)q * rows4; };
-            auto soffb = [&](int ti) __attribute__((always_inline)) { return (uint32_t)ti * 8u * rows4; };
+        // whole tiles: one epilogue per activation, so no flag test sits in the per-element code
+        auto whole_epi = [&](auto act_tag) __attribute__((always_inline)) {
+            constexpr int ACT = decltype(act_tag)::value;
+            // every access in range: one 16- or 8-byte store (and load) per lane and 4 rows, no
+            // branches, so the instruction count below is exact
+            // (a scalar base per row group plus a 32-bit lane offset, so each access takes one VGPR
+            // of address)
+            constexpr size_t kElt = OUT_LP ? 2u : 4u;
+            char* const tb = static_cast<char*>(g.c) + (size_t)(m0 + 128 * wm) * g.ldc * kElt;
+            const uint32_t lo = ((uint32_t)er * (uint32_t)g.ldc + (uint32_t)col0) * (uint32_t)kElt;
+            // row 32 ti + 4 q of the wave's block
+            auto at = [&](int ti, int q) __attribute__((always_inline)) {
+                return tb + (size_t)(32 * ti + 4 * q) * g.ldc * kElt + lo;
+            };
             if (accumulate) {
-                u32x4 cv[2][8];
+                // C in halves of 4 row groups, each half's loads issued before the previous half's
+                // stores (a load waited for behind older stores would wait for them too)
+                u32x4 cv[2][4];
 #pragma unroll
-                for (int q = 0; q < 8; q++) cv[0][q] = __builtin_amdgcn_raw_buffer_load_b128(rc, voffq(q), soffb(0), 0);
+                for (int q = 0; q < 4; q++) cv[0][q] = *reinterpret_cast<const u32x4*>(at(0, q));
 #pragma unroll
                 for (int ti = 0; ti < kTM; ti++) {
-                    to_lds(ti);  // frees acc[ti] before the next block's loads take registers
-                    if (ti + 1 < kTM) {
-#pragma unroll
-                        for (int q = 0; q < 8; q++)
-                            cv[(ti + 1) & 1][q] = __builtin_amdgcn_raw_buffer_load_b128(rc, voffq(q), soffb(ti + 1), 0);
-                    }
+                    to_lds(ti);  // frees acc[ti] before more loads take registers
 #pragma unroll
                     for (int h = 0; h < 2; h++) {
+                        const int hx = 2 * ti + h;  // this half; the next is hx + 1
+                        if (hx + 1 < 2 * kTM) {
+#pragma unroll
+                            for (int q = 0; q < 4; q++)
+                                cv[(hx + 1) & 1][q] = *reinterpret_cast<const u32x4*>(at((hx + 1) / 2, 4 * ((hx + 1) % 2) + q));
+                        }
                         floatx4 vv[4];
                         rows(4 * h, 4, vv);
 #pragma unroll
-                        for (int q = 4 * h; q < 4 * h + 4; q++) {
-                            const floatx4 v = finish(vv[q - 4 * h]) + __builtin_bit_cast(floatx4, cv[ti & 1][q]);
-                            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rc, voffq(q), soffb(ti), 0);
+                        for (int q = 0; q < 4; q++) {
+                            const floatx4 v = activate<ACT>(vv[q], b4) + __builtin_bit_cast(floatx4, cv[hx & 1][q]);
+                            *reinterpret_cast<floatx4*>(at(ti, 4 * h + q)) = v;
                         }
                     }
                     asm volatile("" ::: "memory");
@@ -272,19 +289,28 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_lp(const GemmLpArgs g, uint3
                     to_rows(ti, vv);
 #pragma unroll
                     for (int q = 0; q < 8; q++) {
-                        const floatx4 v = finish(vv[q]);
+                        const floatx4 v = activate<ACT>(vv[q], b4);
                         if (OUT_LP) {
                             floatx4 sv;
 #pragma unroll
                             for (int u = 0; u < 4; u++) sv[u] = clamp_finite(v[u], Enc<T>::kMax);
-                            __builtin_amdgcn_raw_buffer_store_b64(narrow4<T>(sv), rc, voffq(q), soffb(ti), 0);
+                            *reinterpret_cast<u32x2*>(at(ti, q)) = narrow4<T>(sv);
                         } else {
-                            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rc, voffq(q), soffb(ti), 0);
+                            *reinterpret_cast<floatx4*>(at(ti, q)) = v;
                         }
                     }
                     asm volatile("" ::: "memory");
                 }
                 younger = 32;  // 32 stores
+            }
+        };
+        if (whole) {
+            if (g.flags & kGemmSilu) {
+                whole_epi(std::integral_constant<int, 1>{});
+            } else if (g.flags & kGemmRelu) {
+                whole_epi(std::integral_constant<int, 2>{});
+            } else {
+                whole_epi(std::integral_constant<int, 0>{});
             }
         } else {
 #pragma unroll
