@@ -402,6 +402,39 @@ int jc_c2_residual(jc_ctx *ctx, const float *x, int m, int din, const float *w_h
                    const float *w_output, const float *b_output, const float *w_residual, const float *b_residual,
                    int dff, int dout, float *scratch, float *out);
 
+/* ---- The rest of the Timestral block (fp32 unless stated) ------------------------------------- */
+
+/*
+ * out [m, dout] = output(SiLU(hidden(x))) + residual(x): a Timestral ResidualBlock (the patch
+ * embedding and the quantile head), as TimestralForward.Plan.residual queues it
+ * (J/timestral/tornado/TimestralForward.java:397-401; CPU CpuTimestral.Residual.apply,
+ * J/timestral/cpu/CpuTimestral.java:58-71). Arguments as jc_c2_residual.
+ */
+int jc_ts_residual(jc_ctx *ctx, const float *x, int m, int din, const float *w_hidden, const float *b_hidden,
+                   const float *w_output, const float *b_output, const float *w_residual, const float *b_residual,
+                   int dff, int dout, float *scratch, float *out);
+
+/*
+ * x [rows*n, d]: row r's encoder tokens t < enc from emb [rows*enc, d], its decoder tokens
+ * enc <= t < n the forecast query [d]: TimestralKernels.assembleTokens
+ * (J/timestral/tornado/TimestralKernels.java:53-69). d a multiple of 4; 16-byte aligned.
+ */
+int jc_ts_assemble(jc_ctx *ctx, const float *emb, const float *query, float *x, int rows, int enc, int n, int d);
+
+/*
+ * dec [rows*h, d] = the decoder tokens enc..enc+h-1 of every row of y [rows*n, d]:
+ * TimestralKernels.gatherDecoder (J/timestral/tornado/TimestralKernels.java:581-590).
+ * enc + h <= n; d a multiple of 4; 16-byte aligned.
+ */
+int jc_ts_gather_decoder(jc_ctx *ctx, const float *y, float *dec, int rows, int enc, int n, int h, int d);
+
+/*
+ * act [tokens, f] = SiLU(up[t][j]) * up[t][f + j] with up [tokens, 2f], computed in fp32:
+ * Kernels.swiGlu and, for dtype JC_BF16 / JC_F16, Kernels.swiGluHalf with the result saturated to the
+ * type's finite range (J/tornado/Kernels.java:832-856). up and act are both of `dtype`.
+ */
+int jc_swiglu(jc_ctx *ctx, const void *up, void *act, int64_t tokens, int f, int dtype);
+
 #ifdef __cplusplus
 }
 #endif

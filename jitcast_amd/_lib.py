@@ -81,6 +81,10 @@ SIGNATURES = {
     "jc_to_lp": (_i, [_vp, _vp, _vp, _c.c_int64, _i]),
     "jc_c2_assemble": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i]),
     "jc_c2_gather_future": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i]),
+    "jc_ts_residual": (_i, [_vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp]),
+    "jc_ts_assemble": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i]),
+    "jc_ts_gather_decoder": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i]),
+    "jc_swiglu": (_i, [_vp, _vp, _vp, _i64, _i, _i]),
     "jc_c2_prep": (_i, [_vp, _vp, _i64, _i, _vp, _i64, _i, _vp, _i, _i, _i, _i, _i, _f, _i, _vp, _vp, _vp, _vp]),
     "jc_c2_finish": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
     "jc_c2_residual": (_i, [_vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp]),

@@ -864,17 +864,74 @@ int jc_c2_gather_future(jc_ctx* ctx, const float* y, float* dec, int rows, int f
     return e == hipSuccess ? JC_OK : hip_fail(W, e);
 }
 
-int jc_c2_residual(jc_ctx* ctx, const float* x, int m, int din, const float* w_hidden, const float* b_hidden,
-                   const float* w_output, const float* b_output, const float* w_residual, const float* b_residual, int dff,
-                   int dout, float* scratch, float* out) {
-    const char* W = "jc_c2_residual";
+// a residual block as the plans queue it: hidden with the activation into scratch, output into out,
+// residual accumulated into out
+static int residual_block(jc_ctx* ctx, const char* W, const float* x, int m, int din, const float* w_hidden,
+                          const float* b_hidden, const float* w_output, const float* b_output, const float* w_residual,
+                          const float* b_residual, int dff, int dout, float* scratch, float* out, int act) {
     int rc = use(ctx, W);
     if (rc) return rc;
     if (!scratch || !w_hidden || !w_output || !w_residual) return fail(JC_EINVAL, "%s: null weight or scratch", W);
-    // Plan.residual: hidden with ReLU into scratch, output into out, residual accumulated into out
-    if ((rc = launch_linear(ctx, W, x, din, w_hidden, b_hidden, scratch, dff, m, dff, din, JC_GEMM_RELU))) return rc;
+    if ((rc = launch_linear(ctx, W, x, din, w_hidden, b_hidden, scratch, dff, m, dff, din, act))) return rc;
     if ((rc = launch_linear(ctx, W, scratch, dff, w_output, b_output, out, dout, m, dout, dff, 0))) return rc;
     return launch_linear(ctx, W, x, din, w_residual, b_residual, out, dout, m, dout, din, JC_GEMM_ACCUMULATE);
+}
+
+int jc_c2_residual(jc_ctx* ctx, const float* x, int m, int din, const float* w_hidden, const float* b_hidden,
+                   const float* w_output, const float* b_output, const float* w_residual, const float* b_residual, int dff,
+                   int dout, float* scratch, float* out) {
+    // Chronos2Forward.Plan.residual: ReLU hidden layer
+    return residual_block(ctx, "jc_c2_residual", x, m, din, w_hidden, b_hidden, w_output, b_output, w_residual,
+                          b_residual, dff, dout, scratch, out, JC_GEMM_RELU);
+}
+
+int jc_ts_residual(jc_ctx* ctx, const float* x, int m, int din, const float* w_hidden, const float* b_hidden,
+                   const float* w_output, const float* b_output, const float* w_residual, const float* b_residual, int dff,
+                   int dout, float* scratch, float* out) {
+    // TimestralForward.Plan.residual: SiLU hidden layer
+    return residual_block(ctx, "jc_ts_residual", x, m, din, w_hidden, b_hidden, w_output, b_output, w_residual,
+                          b_residual, dff, dout, scratch, out, JC_GEMM_SILU);
+}
+
+int jc_ts_assemble(jc_ctx* ctx, const float* emb, const float* query, float* x, int rows, int enc, int n, int d) {
+    const char* W = "jc_ts_assemble";
+    int rc = use(ctx, W);
+    if (rc) return rc;
+    if (rows < 0 || enc < 0 || enc > n || d <= 0)
+        return fail(JC_EINVAL, "%s: sizes (rows=%d enc=%d n=%d d=%d)", W, rows, enc, n, d);
+    if ((size_t)rows * n == 0) return JC_OK;
+    if (d % 4) return fail(JC_EINVAL, "%s: d must be a multiple of 4 (got %d)", W, d);
+    if (!x || (enc && !emb) || (n > enc && !query)) return fail(JC_EINVAL, "%s: null buffer", W);
+    if (!aligned16(x) || (emb && !aligned16(emb)) || (query && !aligned16(query)))
+        return fail(JC_EINVAL, "%s: 16-byte alignment", W);
+    hipError_t e = jc::ts_assemble_launch(emb, query, x, rows, enc, n, d, ctx->stream);
+    return e == hipSuccess ? JC_OK : hip_fail(W, e);
+}
+
+int jc_ts_gather_decoder(jc_ctx* ctx, const float* y, float* dec, int rows, int enc, int n, int h, int d) {
+    const char* W = "jc_ts_gather_decoder";
+    int rc = use(ctx, W);
+    if (rc) return rc;
+    if (rows < 0 || enc < 0 || h < 0 || enc + h > n || d <= 0)
+        return fail(JC_EINVAL, "%s: sizes (rows=%d enc=%d h=%d n=%d d=%d)", W, rows, enc, h, n, d);
+    if ((size_t)rows * h == 0) return JC_OK;
+    if (d % 4) return fail(JC_EINVAL, "%s: d must be a multiple of 4 (got %d)", W, d);
+    if (!y || !dec) return fail(JC_EINVAL, "%s: null buffer", W);
+    if (!aligned16(y) || !aligned16(dec)) return fail(JC_EINVAL, "%s: 16-byte alignment", W);
+    hipError_t e = jc::gather_future_launch(y, dec, rows, enc, n, h, d, ctx->stream);
+    return e == hipSuccess ? JC_OK : hip_fail(W, e);
+}
+
+int jc_swiglu(jc_ctx* ctx, const void* up, void* act, int64_t tokens, int f, int dtype) {
+    const char* W = "jc_swiglu";
+    int rc = use(ctx, W);
+    if (rc) return rc;
+    if (dtype != JC_F32 && dtype != JC_BF16 && dtype != JC_F16) return fail(JC_EINVAL, "%s: unknown dtype %d", W, dtype);
+    if (tokens < 0 || f < 0) return fail(JC_EINVAL, "%s: negative size (tokens=%lld f=%d)", W, (long long)tokens, f);
+    if (tokens * (int64_t)f == 0) return JC_OK;
+    if (!up || !act) return fail(JC_EINVAL, "%s: null up or act", W);
+    hipError_t e = jc::swiglu_launch(up, act, (uint64_t)tokens, f, dtype, ctx->stream);
+    return e == hipSuccess ? JC_OK : hip_fail(W, e);
 }
 
 }  // extern "C"

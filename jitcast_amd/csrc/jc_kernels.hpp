@@ -88,6 +88,12 @@ hipError_t assemble_tokens_launch(const float* emb, const float* reg, float* x, 
                                   hipStream_t stream);
 hipError_t gather_future_launch(const float* y, float* dec, int rows, int fs, int n, int h, int d, hipStream_t stream);
 
+// The Timestral block's elementwise stages (ts_block.hip): token assembly (d a multiple of 4,
+// 16-byte aligned) and SwiGLU (dtype_code 0 fp32, 1 bf16, 2 fp16 for both up and act)
+hipError_t ts_assemble_launch(const float* emb, const float* query, float* x, int rows, int enc, int n, int d,
+                              hipStream_t stream);
+hipError_t swiglu_launch(const void* up, void* act, uint64_t tokens, int f, int dtype_code, hipStream_t stream);
+
 // The Chronos-2 host ends (c2_prep.hip): ModelLayout's cut and live mask plus ModelPrep.of from the
 // raw context rows; ModelPrep.finish into [rows][Q][h*P]. order (nullable) gathers input rows /
 // scatters output rows.

@@ -214,6 +214,62 @@ def c2_forward_raw(tokens, w: dict, live, group, rows, nc, nreg, h, heads, dh, e
     return c2_residual(dec, w, "out", threads)
 
 
+def silu(x) -> np.ndarray:
+    """Ops.silu (J/cpu/Ops.java:68-70): (float) (v / (1.0 + exp(-v))), in double, rounded."""
+    v = _f32(x).astype(np.float64)
+    return (v / (1.0 + np.exp(-v))).astype(np.float32)
+
+
+def swiglu(up, f: int) -> np.ndarray:
+    """CpuTimestral.s MLP activation (CpuTimestral.java:165-172): act[t][j] = silu(up[t][j]) *
+    up[t][f + j], the product in float."""
+    up = _f32(up)
+    return silu(up[:, :f]) * up[:, f:2 * f]
+
+
+def ts_residual(x, w: dict, prefix: str, threads=0) -> np.ndarray:
+    """CpuTimestral.Residual.apply (CpuTimestral.java:58-71): output(SiLU(hidden(x))) + residual(x)."""
+    h = silu(linear(x, w[prefix + "_hidden_w"], w.get(prefix + "_hidden_b"), threads))
+    y = linear(h, w[prefix + "_output_w"], w.get(prefix + "_output_b"), threads)
+    return add(y, linear(x, w[prefix + "_residual_w"], w.get(prefix + "_residual_b"), threads))
+
+
+def ts_forward_raw(tokens, w: dict, key_valid, known, position, group, role, covariates, rows, enc, ll, h, heads,
+                   dh, rope_dim, eps, theta=10000.0, threads=0) -> np.ndarray:
+    """CpuTimestral.predictBlock from the patch tokens to the head's raw outputs
+    (CpuTimestral.java:127-188): the patch embedding, the encoder tokens then h forecast-query tokens
+    per row, per layer each attention sublayer (rmsNorm, q|k|v, time attention with RoPE at
+    `position` or variate attention, the sigmoid gate, the output projection added) and the SwiGLU
+    MLP, the output norm, the decoder tokens, the head. tokens [rows*enc, 2P]; w as
+    jitcast_amd.timestral_model.random_weights lays it out; returns [rows*h, P*Q]."""
+    n = enc + h
+    emb = ts_residual(tokens, w, "embed", threads)
+    d = emb.shape[1]
+    x = np.empty((rows * n, d), np.float32)
+    for i in range(rows):
+        x[i * n: i * n + enc] = emb[i * enc: (i + 1) * enc]
+        x[i * n + enc: (i + 1) * n] = _f32(w["query"])
+    for lw in w["layers"]:
+        for a in lw["attentions"]:
+            hn = rms_norm(x, a["norm"], eps)
+            qkv = linear(hn, a["qkv"], None, threads)
+            if a["time"]:
+                att = ts_time_attention(qkv, key_valid, known, position, rows, enc, ll, n, heads, dh, d, rope_dim, theta,
+                                        threads)
+            else:
+                att = ts_variate_attention(qkv, key_valid, group, role, covariates, rows, enc, n, heads, dh, d, threads)
+            if a.get("gate") is not None:
+                att = ts_gate(att, linear(hn, a["gate"], None, threads))
+            x = add(x, linear(att, a["wo"], None, threads))
+        hn = rms_norm(x, lw["mlp_norm"], eps)
+        f = lw["down"].shape[1]
+        act = swiglu(linear(hn, lw["up"], None, threads), f)
+        x = add(x, linear(act, lw["down"], None, threads))
+    y = rms_norm(x, w["out_norm"], eps)
+    dec = np.concatenate([y[i * n + enc: (i + 1) * n] for i in range(rows)])
+    return ts_residual(dec, w, "head", threads)
+
+
 def c2_instance_norm(row) -> tuple:
     """ModelPrep.instanceNorm (ModelPrep.java:80-101), value by value: mean and population std of the
     observed values in double, rounded to float; a zero std floored at 1e-5; (0, 1) with none."""
