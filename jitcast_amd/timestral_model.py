@@ -14,8 +14,14 @@ TimestralForward.java:327-382).
                       jc_swiglu, jc_linear accumulated), the output norm, the decoder tokens
                       (jc_ts_gather_decoder) and the head (jc_ts_residual)
 
-The host ends (BlockLayout.of through jc_ts_block_layout, BlockPrep, the quantile head's
-monotone map) stay on the host, as in the reference.
+  block_window, block_prep, quantile_map, block_finish
+                      the host ends of predict_block, numpy restatements with the reference's
+                      float/double rounding: BlockLayout.of's window (J/timestral/BlockLayout.java
+                      :77-148), BlockPrep.of (BlockPrep.java:40-75; Scaler.java's causal patch
+                      loc/scale, instance norm, affine), Quantiles.apply (Quantiles.java:52-77) and
+                      BlockPrep.finish (BlockPrep.java:77-101; Scaler.invert, clampNonFinite)
+  HipTimestralModel.predict_block
+                      BlockLayout + BlockPrep on the host, the device forward, finish on the host
 """
 from __future__ import annotations
 
@@ -42,6 +48,12 @@ class TimestralConfig:
     norm_eps: float = 1e-6
     time_attn_gate: bool = True
     variate_attn_gate: bool = True
+    minimum_scale: float = 1e-6
+    use_asinh: bool = True
+    quantile_width_factor: float = 2.0
+    covariate_enabled: bool = True
+    attend_missing: bool = True
+    block_size: int = 64
 
     @property
     def head_dim(self) -> int:
@@ -54,6 +66,10 @@ class TimestralConfig:
     @property
     def num_quantiles(self) -> int:
         return len(self.quantiles)
+
+    @property
+    def median_index(self) -> int:
+        return self.quantiles.index(0.5)
 
 
 def random_weights(c: TimestralConfig, seed: int = 0, std: float = 0.02) -> dict:
@@ -171,3 +187,186 @@ class HipTimestralModel:
                   p(w["head_output_w"]), None, p(w["head_residual_w"]), None, 4 * d, c.patch_size * c.num_quantiles,
                   p(b["scratch"]), p(b["raw"]))
         return b["raw"]
+
+    def predict_block(self, inputs, observed, group, h: int, role=None, known_future=None, known_future_mask=None):
+        """TimestralModel.predict_block on one block, as CpuTimestral.predictBlock runs it
+        (J/timestral/cpu/CpuTimestral.java:127-188): BlockLayout (jc_ts_block_layout) and BlockPrep
+        on the host, the device forward, BlockPrep.finish on the host. inputs / observed [rows, t]
+        (t a multiple of the patch), group [rows] with each series' rows contiguous, h forecast
+        patches, role [rows] (0 TARGET, 1 PAST, 2 KNOWN) and the known covariates' future steps
+        [rows, h*P] for a covariate block. Returns [rows, h*P, Q] quantiles."""
+        import torch
+
+        c = self.c
+        ps = c.patch_size
+        window, obs, cov = block_window(c, inputs, observed, role, known_future, known_future_mask, h)
+        rows, t = np.asarray(inputs).shape
+        enc, cov_l, kv, known, pos = timestral.block_layout(
+            observed, group, h, ps, role=role if cov else None, future_observed=known_future_mask if cov else None,
+            covariate_enabled=c.covariate_enabled, attend_missing=c.attend_missing, block_size=c.block_size)
+        if enc != window.shape[1] // ps or cov_l != cov:
+            raise _lib.JitcastError(_lib.JC_EINVAL, "block layout and window disagree")
+        tok, _, loc, scale = block_prep(c, window, obs, known)
+        gs, ge = chronos2.group_bounds(group)
+        up = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.int32)).to(self.dev)  # noqa: E731
+        raw = self.forward_raw(torch.from_numpy(tok).to(self.dev), up(kv.reshape(-1)), up(known), up(pos.reshape(-1)),
+                               up(gs), up(ge), up(role) if cov else None, cov, rows, enc, h)
+        return block_finish(c, raw.cpu().numpy(), loc, scale, t // ps, h)
+
+
+FLOAT32_EPS = np.float32(np.finfo(np.float32).eps)
+
+
+def block_window(c: TimestralConfig, inputs, observed, role=None, known_future=None, known_future_mask=None,
+                 h: int = 1):
+    """BlockLayout.of's window (BlockLayout.java:77-109): the context rows, plus the horizon's known
+    future steps when the block runs the covariate path (role given, covariates enabled, some row not
+    a TARGET). Returns (window float32 [rows, w], observed bool [rows, w], covariates)."""
+    x = np.ascontiguousarray(inputs, dtype=np.float32)
+    obs = np.ascontiguousarray(observed, dtype=bool)
+    rows, t = x.shape
+    if t % c.patch_size:
+        raise _lib.JitcastArgumentError(_lib.JC_EINVAL, f"context length {t} is not a multiple of the patch size")
+    if h < 1:
+        raise _lib.JitcastArgumentError(_lib.JC_EINVAL, f"horizon patches must be >= 1, got {h}")
+    cov = role is not None and c.covariate_enabled and bool(np.any(np.asarray(role) != 0))
+    if not cov:
+        return x, obs, False
+    if h > c.block_size:
+        raise _lib.JitcastArgumentError(_lib.JC_EINVAL, f"a block with covariates decodes at most {c.block_size} patches")
+    w = t + h * c.patch_size
+    win = np.zeros((rows, w), np.float32)
+    ob = np.zeros((rows, w), bool)
+    win[:, :t], ob[:, :t] = x, obs
+    if known_future is not None:
+        win[:, t:] = np.asarray(known_future, np.float32)[:, : h * c.patch_size]
+        ob[:, t:] = np.asarray(known_future_mask, bool)[:, : h * c.patch_size]
+    return win, ob, True
+
+
+def _causal_patch_loc_scale(x, obs, patch, minimum_scale):
+    """Scaler.causalPatchLocScale (Scaler.java:40-64), all rows at once: a running weighted mean and
+    Welford M2 in double; at each patch end, loc = mean and scale = max(sqrt(M2 / max(max(w,1)-1,1)),
+    minimum) rounded to float for the patch's steps."""
+    rows, t = x.shape
+    ms = np.float64(np.float32(minimum_scale))  # the config's float, widened as Java widens it
+    xd = x.astype(np.float64)
+    wd = obs.astype(np.float64)
+    cum_w = np.zeros(rows)
+    cum_x = np.zeros(rows)
+    m2 = np.zeros(rows)
+    prev = np.zeros(rows)
+    loc = np.empty((rows, t), np.float32)
+    scale = np.empty((rows, t), np.float32)
+    for i in range(t):
+        cum_w += wd[:, i]
+        cum_x += wd[:, i] * xd[:, i]
+        mean = cum_x / np.maximum(cum_w, 1.0)
+        m2 += (xd[:, i] - prev) * (xd[:, i] - mean) * wd[:, i]
+        prev = mean
+        if i % patch == patch - 1:
+            var = m2 / np.maximum(np.maximum(cum_w, 1.0) - 1.0, 1.0)
+            loc[:, i - patch + 1: i + 1] = mean.astype(np.float32)[:, None]
+            scale[:, i - patch + 1: i + 1] = np.maximum(np.sqrt(var), ms).astype(np.float32)[:, None]
+    return loc, scale
+
+
+def _instance_norm(x, obs, minimum_scale):
+    """Scaler.instanceNorm (Scaler.java:87-110) for one row: (loc, scale, binary) in float from sums
+    in double; a row of observed 0/1 values gives (0, 1, binary)."""
+    n = max(float(np.count_nonzero(obs)), 1.0)
+    loc = np.float32(np.sum(x[obs].astype(np.float64)) / n)
+    d = np.where(obs, x - loc, np.float32(0)).astype(np.float32)
+    ss = float(np.sum(d.astype(np.float64) ** 2))
+    scale = max(np.float32(np.sqrt(np.float32(ss / n))), np.float32(minimum_scale))
+    binary = bool(np.all((x == 0) | (x == 1) | ~obs)) and bool(np.any(obs))
+    return (np.float32(0), np.float32(1), True) if binary else (loc, np.float32(scale), False)
+
+
+def _asinh(v):
+    a = np.abs(v.astype(np.float64))
+    r = np.log(a + np.sqrt(a * a + 1.0))
+    return np.where(v < 0, -r, r).astype(np.float32)
+
+
+def block_prep(c: TimestralConfig, window, obs, known_rows):
+    """BlockPrep.of (BlockPrep.java:40-75): per row the causal patch scaler (whole-row instance norm
+    for known covariates), the scaled window (0 where unobserved, arcsinh unless a binary covariate)
+    and the embedding input of every encoder token [values, missing flags]. Returns (tokens
+    [rows*enc, 2P], scaled, loc, scale [rows, w])."""
+    ps = c.patch_size
+    rows, w = window.shape
+    enc = w // ps
+    loc, scale = _causal_patch_loc_scale(window, obs, ps, c.minimum_scale)
+    asinh_row = np.full(rows, c.use_asinh)
+    for i in np.flatnonzero(np.asarray(known_rows, bool)):
+        lo, sc, binary = _instance_norm(window[i], obs[i], c.minimum_scale)
+        loc[i], scale[i] = lo, sc
+        asinh_row[i] = c.use_asinh and not binary
+    v = ((window - loc) / np.maximum(scale, FLOAT32_EPS)).astype(np.float32)
+    v = np.where(asinh_row[:, None], _asinh(v), v)
+    scaled = np.where(obs, v, np.float32(0)).astype(np.float32)
+    tok = np.empty((rows, enc, 2 * ps), np.float32)
+    tok[:, :, :ps] = scaled.reshape(rows, enc, ps)
+    tok[:, :, ps:] = np.where(obs, np.float32(0), np.float32(1)).reshape(rows, enc, ps)
+    return tok.reshape(rows * enc, 2 * ps), scaled, loc, scale
+
+
+def _softplus(x):
+    xd = x.astype(np.float64)
+    return np.where(x > 20, x, np.log1p(np.exp(np.minimum(xd, 20.0))).astype(np.float32)).astype(np.float32)
+
+
+def quantile_map(c: TimestralConfig, raw):
+    """Quantiles.apply (Quantiles.java:52-77) on every row of raw [..., Q]: the median kept, each
+    level above it the median plus the running sum of widthFactor*dp*softplus(raw), each level
+    below minus it, clamped to the finite float range. Widths rounded to float as the reference's
+    tensor holds them."""
+    knots = np.asarray(c.quantiles, np.float64)
+    q = len(knots)
+    med = c.median_index
+    width = np.zeros(q, np.float32)
+    for i in range(q):
+        width[i] = np.float32(knots[i] - knots[i - 1] if i > med else knots[i + 1] - knots[i] if i < med else 0.0)
+    width = (np.float32(c.quantile_width_factor) * width).astype(np.float32)
+    raw = np.asarray(raw, np.float32)
+    out = np.empty_like(raw)
+    m = raw[..., med]
+    big = np.float32(np.finfo(np.float32).max)
+    up = np.zeros(m.shape, np.float32)
+    for i in range(med + 1, q):
+        up = (up + width[i] * _softplus(raw[..., i])).astype(np.float32)
+        out[..., i] = np.clip(m + up, -big, big)
+    down = np.zeros(m.shape, np.float32)
+    for i in range(med - 1, -1, -1):
+        down = (down + width[i] * _softplus(raw[..., i])).astype(np.float32)
+        out[..., i] = np.clip(m - down, -big, big)
+    out[..., med] = np.clip(m, -big, big)
+    return out
+
+
+def _clamp_non_finite(v):
+    """Scaler.clampNonFinite (Scaler.java:118-130) over the last axis: +inf to the finite max, -inf
+    to the finite min, 0 where no finite value exists."""
+    fin = np.isfinite(v)
+    vmax = np.where(fin, v, -np.inf).max(axis=-1, keepdims=True)
+    vmin = np.where(fin, v, np.inf).min(axis=-1, keepdims=True)
+    x = np.where(v == np.inf, vmax, np.where(v == -np.inf, vmin, v))
+    return np.where(np.isinf(x), np.float32(0), x).astype(np.float32)
+
+
+def block_finish(c: TimestralConfig, raw, loc, scale, ll: int, h: int):
+    """BlockPrep.finish (BlockPrep.java:77-101): the quantile map on raw [rows*h, P*Q] (steps
+    P-major, Q levels contiguous), then each step denormalized with the frame of the last context
+    patch (sinh when the scaler used arcsinh; float multiply then add) and non-finite values clamped.
+    Returns [rows, h*P, Q]."""
+    ps, q = c.patch_size, c.num_quantiles
+    rows = loc.shape[0]
+    v = quantile_map(c, np.asarray(raw, np.float32).reshape(rows, h * ps, q))
+    a_loc = loc[:, (ll - 1) * ps][:, None, None]
+    a_scale = scale[:, (ll - 1) * ps][:, None, None]
+    with np.errstate(over="ignore"):
+        if c.use_asinh:
+            v = np.sinh(v.astype(np.float64)).astype(np.float32)
+        out = (v * a_scale).astype(np.float32) + a_loc
+    return _clamp_non_finite(out.astype(np.float32))

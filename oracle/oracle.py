@@ -270,6 +270,131 @@ def ts_forward_raw(tokens, w: dict, key_valid, known, position, group, role, cov
     return ts_residual(dec, w, "head", threads)
 
 
+def ts_block_prep(window, observed, known, patch, minimum_scale, use_asinh):
+    """BlockPrep.of (J/timestral/BlockPrep.java:40-75) value by value: Scaler.causalPatchLocScale
+    (Scaler.java:40-64) for every row, Scaler.instanceNorm (Scaler.java:87-110) for known covariate
+    rows (arcsinh off for a binary one), Scaler.affine (Scaler.java:73-79). Returns (tokens
+    [rows*enc, 2P], scaled, loc, scale [rows, w])."""
+    window = _f32(window)
+    rows, w = window.shape
+    enc = w // patch
+    f32 = np.float32
+    ms = float(f32(minimum_scale))
+    eps = float(np.finfo(np.float32).eps)
+    loc = np.zeros((rows, w), f32)
+    scale = np.zeros((rows, w), f32)
+    scaled = np.zeros((rows, w), f32)
+    tok = np.zeros((rows * enc, 2 * patch), f32)
+    for i in range(rows):
+        cw = cx = m2 = prev = 0.0
+        for t in range(w):
+            wt = 1.0 if observed[i][t] else 0.0
+            xi = float(window[i][t])
+            cw += wt
+            cx += wt * xi
+            mean = cx / max(cw, 1.0)
+            m2 += (xi - prev) * (xi - mean) * wt
+            prev = mean
+            if t % patch == patch - 1:
+                var = m2 / max(max(cw, 1.0) - 1.0, 1.0)
+                for j in range(t - patch + 1, t + 1):
+                    loc[i][j] = f32(mean)
+                    scale[i][j] = f32(max(float(np.sqrt(var)), ms))
+        asinh = use_asinh
+        if known[i]:
+            n = 0.0
+            total = 0.0
+            zero_one, anyo = True, False
+            for t in range(w):
+                if observed[i][t]:
+                    n += 1
+                    total += float(window[i][t])
+                    anyo = True
+                zero_one = zero_one and (window[i][t] == 0 or window[i][t] == 1 or not observed[i][t])
+            n = max(n, 1.0)
+            lo = f32(total / n)
+            ss = 0.0
+            for t in range(w):
+                dv = f32(window[i][t] - lo) if observed[i][t] else f32(0)
+                ss += float(dv) * float(dv)
+            sc = max(f32(np.sqrt(float(f32(ss / n)))), f32(ms))
+            if zero_one and anyo:
+                lo, sc = f32(0), f32(1)
+                asinh = False
+            loc[i][:] = lo
+            scale[i][:] = sc
+        for t in range(w):
+            if not observed[i][t]:
+                continue
+            v = f32(f32(window[i][t] - loc[i][t]) / max(scale[i][t], f32(eps)))
+            if asinh:
+                a = abs(float(v))
+                r = np.log(a + np.sqrt(a * a + 1.0))
+                v = f32(-r if v < 0 else r)
+            scaled[i][t] = v
+        for p in range(enc):
+            for s in range(patch):
+                tok[i * enc + p][s] = scaled[i][p * patch + s]
+                tok[i * enc + p][patch + s] = f32(0) if observed[i][p * patch + s] else f32(1)
+    return tok, scaled, loc, scale
+
+
+def ts_quantile_map(raw, knots, median, width_factor):
+    """Quantiles.apply (J/timestral/Quantiles.java:52-77) on each row of raw [..., Q], in place order:
+    levels above the median from the median up, below it from the median down."""
+    raw = _f32(raw).reshape(-1, len(knots)).copy()
+    f32 = np.float32
+    q = len(knots)
+    width = [f32(f32(width_factor) * f32(knots[i] - knots[i - 1] if i > median else knots[i + 1] - knots[i]
+                                          if i < median else 0.0)) for i in range(q)]
+    big = float(np.finfo(np.float32).max)
+
+    def softplus(x):
+        return x if x > 20 else f32(np.log1p(np.exp(float(x))))
+
+    for row in raw:
+        m = row[median]
+        up = f32(0)
+        for i in range(median + 1, q):
+            up = f32(up + f32(width[i] * softplus(row[i])))
+            row[i] = f32(min(max(float(f32(m + up)), -big), big))
+        down = f32(0)
+        for i in range(median - 1, -1, -1):
+            down = f32(down + f32(width[i] * softplus(row[i])))
+            row[i] = f32(min(max(float(f32(m - down)), -big), big))
+        row[median] = f32(min(max(float(m), -big), big))
+    return raw
+
+
+def ts_block_finish(raw, loc, scale, ll, h, patch, knots, median, width_factor, use_asinh):
+    """BlockPrep.finish (J/timestral/BlockPrep.java:77-101) value by value: the quantile map on every
+    step's Q raw values, Scaler.invert with the loc/scale of the last context patch's first step
+    (sinh when use_asinh; float multiply, then add), Scaler.clampNonFinite (Scaler.java:118-130) per
+    step. raw [rows*h, P*Q]; returns [rows, h*P, Q]."""
+    rows = np.asarray(loc).shape[0]
+    q = len(knots)
+    f32 = np.float32
+    v = ts_quantile_map(np.asarray(raw, np.float32).reshape(rows * h * patch, q), knots, median, width_factor)
+    v = v.reshape(rows, h * patch, q)
+    out = np.zeros_like(v)
+    for i in range(rows):
+        a_loc, a_scale = f32(loc[i][(ll - 1) * patch]), f32(scale[i][(ll - 1) * patch])
+        for t in range(h * patch):
+            vals = []
+            for k in range(q):
+                x = v[i][t][k]
+                with np.errstate(over="ignore"):
+                    x = f32(np.sinh(float(x))) if use_asinh else x
+                vals.append(f32(f32(x * a_scale) + a_loc))
+            fin = [x for x in vals if np.isfinite(x)]
+            hi = max(fin) if fin else -np.inf
+            lo = min(fin) if fin else np.inf
+            for k, x in enumerate(vals):
+                y = hi if x == np.inf else lo if x == -np.inf else x
+                out[i][t][k] = f32(0) if np.isinf(y) else y
+    return out
+
+
 def c2_instance_norm(row) -> tuple:
     """ModelPrep.instanceNorm (ModelPrep.java:80-101), value by value: mean and population std of the
     observed values in double, rounded to float; a zero std floored at 1e-5; (0, 1) with none."""

@@ -128,3 +128,56 @@ def test_forward_matches_oracle(gpu, oracle, name, c, rows, groups, enc, h, cova
     err = oracle.rel_max_error(raw.cpu().numpy(), exp)
     print(f"  raw rel err {err:.3e}", flush=True)
     assert err <= 1e-4
+
+
+def _oracle_block(oracle, c, x, obs, group, h, role, fut, fut_mask):
+    """CpuTimestral.predictBlock end to end on the oracle's pieces."""
+    ps = c.patch_size
+    window, wobs, cov = tm.block_window(c, x, obs, role, fut, fut_mask, h)
+    enc, _, kv, known, pos = timestral.block_layout(obs, group, h, ps, role=role if cov else None,
+                                                    future_observed=fut_mask if cov else None)
+    tok, _, loc, scale = oracle.ts_block_prep(window, wobs, known, ps, c.minimum_scale, c.use_asinh)
+    rows, t = x.shape
+    ll = t // ps
+    raw = oracle.ts_forward_raw(tok, tm_weights(c), kv, known, pos - enc, group, role if cov else np.zeros(rows, np.int32),
+                                cov, rows, enc, ll, h, c.num_heads, c.head_dim, c.rope_dim, c.norm_eps, c.rope_theta)
+    return oracle.ts_block_finish(raw, loc, scale, ll, h, ps, c.quantiles, c.median_index, c.quantile_width_factor,
+                                  c.use_asinh)
+
+
+_W = {}
+
+
+def tm_weights(c):
+    if c not in _W:
+        _W[c] = tm.random_weights(c, seed=11, std=0.1)
+    return _W[c]
+
+
+@pytest.mark.parametrize("covariates", [False, True])
+def test_predict_block_matches_oracle(gpu, oracle, covariates):
+    """BlockLayout + BlockPrep + device forward + finish against the oracle's CpuTimestral restatement,
+    quantiles within 1e-3 (the north star's end-to-end bar)."""
+    c = tm.TimestralConfig(patch_size=8, d_model=64, num_heads=2, mlp_hidden_dim=96,
+                           layers=((True, False), (True, False)), quantiles=(0.1, 0.5, 0.9), block_size=4)
+    print(f"case predict_block covariates={covariates}", flush=True)
+    r = np.random.default_rng(12)
+    rows, t, h = 6, 48, 3
+    x = (20 + 4 * np.sin(np.arange(t) / 5.0)[None, :] + r.standard_normal((rows, t))).astype(np.float32)
+    obs = r.random((rows, t)) > 0.1
+    obs[1, :20] = False
+    group = np.array([0, 0, 0, 1, 1, 1], np.int32)
+    role = np.array([0, 1, 2, 0, 2, 1], np.int32) if covariates else None
+    fut = fut_mask = None
+    if covariates:
+        fut = r.standard_normal((rows, h * 8)).astype(np.float32)
+        fut_mask = np.zeros((rows, h * 8), bool)
+        fut_mask[role == 2] = True
+    model = tm.HipTimestralModel(c, tm_weights(c))
+    got = model.predict_block(x, obs, group, h, role, fut, fut_mask)
+    exp = _oracle_block(oracle, c, x, obs, group, h, role, fut, fut_mask)
+    assert got.shape == (rows, h * 8, 3)
+    err = oracle.rel_max_error(got, exp)
+    print(f"  quantiles rel err {err:.3e}", flush=True)
+    assert err <= 1e-3
+    assert np.all(np.diff(got, axis=2) >= 0)  # non-crossing

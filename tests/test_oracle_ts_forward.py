@@ -100,3 +100,73 @@ def test_forward_matches_brute_force(oracle, covariates):
     assert got.shape == (rows * h, c.patch_size * c.num_quantiles)
     err = np.max(np.abs(got - exp)) / np.max(np.abs(exp))
     assert err < 2e-5, err
+
+
+# ---- the host ends: BlockPrep.of / Quantiles.apply / BlockPrep.finish ---------------------------------
+
+def test_prep_closed_forms(oracle):
+    """A constant row: loc = the value, the causal std 0 floored at minimum_scale, so observed steps
+    scale to 0; a binary known covariate: (0, 1) and no arcsinh; an unobserved step: 0 and a missing
+    flag."""
+    ps = 4
+    window = np.array([[5.0] * 8, [0, 1, 1, 0, 1, 0, 0, 1], [1.0, 2, 3, 4, 5, 6, 7, 8]], np.float32)
+    obs = np.ones((3, 8), bool)
+    obs[2, 5] = False
+    tok, scaled, loc, scale = oracle.ts_block_prep(window, obs, [0, 1, 0], ps, 1e-6, True)
+    assert np.all(loc[0] == 5) and np.all(scale[0] == np.float32(1e-6)) and np.all(scaled[0] == 0)
+    assert np.all(loc[1] == 0) and np.all(scale[1] == 1)
+    np.testing.assert_array_equal(scaled[1], window[1])  # binary: (x - 0) / 1, no arcsinh
+    # causal patch frames of a ramp: patch 0 mean 2.5, sample std sqrt(5/3)
+    assert loc[2][0] == np.float32(2.5) and scale[2][0] == np.float32(np.sqrt(5.0 / 3.0))
+    assert scaled[2][5] == 0 and tok[2 * 2 + 1][ps + 1] == 1 and tok[2 * 2 + 1][1] == 0
+    assert scaled[2][0] == np.float32(np.arcsinh(np.float32((1.0 - 2.5) / np.float32(np.sqrt(5.0 / 3.0)))))
+
+
+def test_quantile_map_closed_forms(oracle):
+    """Zero raw deltas: softplus(0) = ln 2, so level i sits width_factor * ln 2 * (cumulative dp)
+    from the median; large raw deltas pass through softplus as themselves."""
+    knots = (0.1, 0.5, 0.9)
+    raw = np.array([[0.0, 3.0, 0.0], [25.0, -1.0, 30.0]], np.float32)
+    got = oracle.ts_quantile_map(raw, knots, 1, 2.0)
+    w = np.float32(2.0) * np.float32(0.4)
+    ln2 = np.float32(np.log1p(np.exp(0.0)))
+    np.testing.assert_array_equal(got[0], [np.float32(3.0) - np.float32(w * ln2), 3.0, np.float32(3.0) + np.float32(w * ln2)])
+    np.testing.assert_array_equal(got[1], [np.float32(-1.0) - np.float32(w * 25), -1.0, np.float32(-1.0) + np.float32(w * 30)])
+    assert np.all(np.diff(got, axis=1) >= 0)
+
+
+def _block(seed, rows, t, ps, nan_frac=0.1):
+    r = np.random.default_rng(seed)
+    x = (10 + 3 * r.standard_normal((rows, t))).astype(np.float32)
+    obs = r.random((rows, t)) >= nan_frac
+    obs[0, : ps + 1] = False
+    return x, obs
+
+
+@pytest.mark.parametrize("asinh", [True, False])
+def test_host_prep_matches_oracle(oracle, asinh):
+    c = tm.TimestralConfig(patch_size=4, use_asinh=asinh, quantiles=(0.1, 0.5, 0.9))
+    x, obs = _block(3, 5, 24, 4)
+    x[3] = (x[3] > 10).astype(np.float32)  # a binary row
+    known = np.array([0, 0, 1, 1, 0])
+    tok, scaled, loc, scale = tm.block_prep(c, x, obs, known)
+    e_tok, e_scaled, e_loc, e_scale = oracle.ts_block_prep(x, obs, known, 4, c.minimum_scale, asinh)
+    np.testing.assert_array_max_ulp(loc, e_loc, maxulp=1)
+    np.testing.assert_array_max_ulp(scale, e_scale, maxulp=1)
+    np.testing.assert_array_max_ulp(tok, e_tok, maxulp=2)
+    np.testing.assert_array_max_ulp(scaled, e_scaled, maxulp=2)
+
+
+def test_host_finish_matches_oracle(oracle):
+    c = tm.TimestralConfig(patch_size=4, quantiles=(0.1, 0.2, 0.5, 0.8, 0.9))
+    r = np.random.default_rng(4)
+    rows, h, ll = 3, 2, 5
+    raw = r.standard_normal((rows * h, 4 * 5)).astype(np.float32)
+    raw[0, 2] = 89.0  # step 0's median: sinh(89) is finite, the levels above overflow and are clamped
+    loc = (5 + r.standard_normal((rows, 6 * 4))).astype(np.float32)
+    scale = np.abs(r.standard_normal((rows, 6 * 4))).astype(np.float32) + np.float32(0.1)
+    got = tm.block_finish(c, raw, loc, scale, ll, h)
+    exp = oracle.ts_block_finish(raw, loc, scale, ll, h, 4, c.quantiles, c.median_index, c.quantile_width_factor, True)
+    assert np.all(np.isfinite(got))
+    assert got[0, 0, 4] == got[0, 0, 2] > 1e37  # +inf clamped to the step's finite maximum
+    np.testing.assert_array_max_ulp(got, exp, maxulp=2)
