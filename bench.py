@@ -293,6 +293,64 @@ def forecast_line(steps: int, warmup: int, dtype_name: str = "f32") -> dict:
     return res
 
 
+def ts_block_line(steps: int, warmup: int, dtype_name: str = "f32") -> dict:
+    """The Timestral block end to end at config 3's shape: HipTimestralModel.predict_block on 64
+    univariate series of 1023 patches (16,368 steps, left padding U{0..256} patches unobserved) and
+    one forecast patch, 1024 tokens per series, a 123M-class model (d_model 768, 12 x 64, 12 layers
+    of time + variate attention with gates, SwiGLU MLP 3072), random-init weights; fp32 or the
+    FP16-GEMM mode in bf16.
+    value = series per second, wall clock around predict_block (host BlockLayout and BlockPrep, the
+    device forward, the host finish); the device forward alone timed with HIP events."""
+    import numpy as np
+    import torch
+
+    from jitcast_amd import rng, timestral
+    from jitcast_amd import timestral_model as tm
+
+    c = tm.TimestralConfig()
+    model = tm.HipTimestralModel(c, tm.random_weights(c, seed=0), dtype=dtype_name)
+    rows, patches, h = 64, 1023, 1
+    t = patches * c.patch_size
+    x = rng.normal(rng.stream_seed(3, 0), rows * t, 1.0).reshape(rows, t).astype(np.float32)
+    pad = rng.randint(rng.stream_seed(3, 1), rows, 0, 256)
+    obs = np.arange(t)[None, :] >= (pad * c.patch_size)[:, None]
+    group = np.arange(rows, dtype=np.int32)
+    for _ in range(warmup):
+        model.predict_block(x, obs, group, h)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        out = model.predict_block(x, obs, group, h)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / steps
+    enc, _, kv, known, pos = timestral.block_layout(obs, group, h, c.patch_size)
+    tok, _, _, _ = tm.block_prep(c, x, obs, known)
+    gs, ge = tm.chronos2.group_bounds(group)
+    up = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(model.dev)  # noqa: E731
+    args = (up(tok), up(kv.reshape(-1)), up(known), up(pos.reshape(-1)), up(gs), up(ge), None, False, rows, enc, h)
+    dev_ms = time_launches(lambda: model.forward_raw(*args), max(2, steps), 1)
+    assert np.isfinite(out).all()
+    n = enc + h
+    d, f = c.d_model, c.mlp_hidden_dim
+    gemm_flops = 2.0 * rows * n * len(c.layers) * (2 * 5 * d * d + 3 * f * d)
+    log(f"ts block {dtype_name}: {wall * 1e3:.1f} ms per predict_block ({rows / wall:.0f} series/s), device forward "
+        f"{dev_ms:.1f} ms ({rows / (dev_ms * 1e-3):.0f} series/s, GEMMs {gemm_flops / (dev_ms * 1e-3) / 1e12:.1f} TFLOP/s)")
+    res = {
+        "workload": f"config 3 shape: Timestral 123M-class block forward ({dtype_name}), 64 univariate series x 1023 patches "
+                    "+ 1 forecast patch (1024 tokens), left padding U{0..256} patches, random-init weights",
+        "metric": "forecast series/sec",
+        "value": round(rows / wall, 1),
+        "unit": "series/s",
+        "ms_per_call": round(wall * 1e3, 2),
+        "device_forward_ms": round(dev_ms, 2),
+        "device_series_per_s": round(rows / (dev_ms * 1e-3), 1),
+        "gemm_tflops": round(gemm_flops / (dev_ms * 1e-3) / 1e12, 2),
+    }
+    del model
+    torch.cuda.empty_cache()
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -300,7 +358,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=256)
-    ap.add_argument("--only", choices=["all", "time", "group", "bf16", "fp16", "layer", "layer-bf16", "ts", "forecast"], default="all",
+    ap.add_argument("--only", choices=["all", "time", "group", "bf16", "fp16", "layer", "layer-bf16", "ts", "ts-block", "forecast"], default="all",
                     help="which workloads to run (profiling runs select one kernel)")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="only run 5 plain device copies of this many bytes (calibrates rocprof byte counters)")
@@ -331,6 +389,12 @@ def main() -> int:
         for name in ("bf16", "f32"):
             also[f"c2_forecast_{name}"] = forecast_line(2, 1, name)
         if args.only == "forecast":
+            print(json.dumps({"also": also}), flush=True)
+            return 0
+    if args.only in ("all", "ts-block"):
+        for name in ("bf16", "f32"):
+            also[f"ts_block_{name}"] = ts_block_line(2, 1, name)
+        if args.only == "ts-block":
             print(json.dumps({"also": also}), flush=True)
             return 0
     if args.only in ("all", "ts"):

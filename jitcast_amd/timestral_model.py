@@ -106,18 +106,34 @@ def random_weights(c: TimestralConfig, seed: int = 0, std: float = 0.02) -> dict
 
 
 class HipTimestralModel:
-    """The Timestral block forward on one GPU, fp32 (the reference's FP32-exact default): weights
-    uploaded once, per-shape buffers kept for the last shape, one call per block."""
+    """The Timestral block forward on one GPU: weights uploaded once, per-shape buffers kept for the
+    last shape, one call per block. dtype "f32" is the reference's FP32-exact default; "bf16" /
+    "fp16" mirror its FP16 GEMM mode (TimestralForward.java:467-499 with Kernels.gemmHalf): the
+    attention sublayers' and the MLP's GEMMs take storage-type operands with fp32 accumulation, the
+    time attention and SwiGLU run in the storage type, the variate attention reads fp32 q|k|v, the
+    residual stream, norms' inputs, the embedding and the head stay fp32."""
 
-    def __init__(self, c: TimestralConfig, weights: dict, device: int = 0):
+    def __init__(self, c: TimestralConfig, weights: dict, dtype: str = "f32", device: int = 0):
         import torch
 
-        self.c = c
+        self.c, self.dtype = c, dtype
+        self.code = {"f32": _lib.JC_F32, "bf16": _lib.JC_BF16, "fp16": _lib.JC_F16}[dtype]
+        self.tdt = {"f32": torch.float32, "bf16": torch.bfloat16, "fp16": torch.float16}[dtype]
         self.dev = torch.device("cuda", device)
         t = lambda a: None if a is None else torch.from_numpy(np.ascontiguousarray(a)).to(self.dev)  # noqa: E731
+
+        def lp(a):  # a weight matrix in the storage type, converted once (Kernels.toHalf)
+            if a is None or self.code == _lib.JC_F32:
+                return t(a)
+            src = t(a)
+            dst = torch.empty(src.shape, dtype=self.tdt, device=self.dev)
+            chronos2.to_lp(src, dst)
+            return dst
+
         self.w = {k: t(v) for k, v in weights.items() if k != "layers"}
-        self.layers = [{"attentions": [{k: (a[k] if k == "time" else t(a[k])) for k in a} for a in lw["attentions"]],
-                        "mlp_norm": t(lw["mlp_norm"]), "up": t(lw["up"]), "down": t(lw["down"])}
+        self.layers = [{"attentions": [{"time": a["time"], "norm": t(a["norm"]), "qkv": lp(a["qkv"]), "gate": lp(a["gate"]),
+                                        "wo": lp(a["wo"])} for a in lw["attentions"]],
+                        "mlp_norm": t(lw["mlp_norm"]), "up": lp(lw["up"]), "down": lp(lw["down"])}
                        for lw in weights["layers"]]
         self._bufs = {}
 
@@ -131,13 +147,18 @@ class HipTimestralModel:
             n, d, f = enc + h, c.d_model, c.mlp_hidden_dim
             tokens = rows * n
             e = lambda *s: torch.empty(*s, dtype=torch.float32, device=self.dev)  # noqa: E731
-            self._bufs[key] = {
+            b = {
                 "emb": e(rows * enc, d), "scratch": e(max(rows * enc, rows * h), 4 * d), "x": e(tokens, d),
                 "hn": e(tokens, d), "big": e(tokens, max(3 * d, 2 * f)), "att": e(tokens, d), "gate": e(tokens, d),
                 "act": e(tokens, f), "y": e(tokens, d), "dec": e(rows * h, d),
                 "raw": e(rows * h, c.patch_size * c.num_quantiles),
                 "table": torch.from_numpy(timestral.rope_table(enc, n, c.head_dim, c.rope_dim, c.rope_theta)).to(self.dev),
             }
+            if self.code != _lib.JC_F32:
+                s = lambda *sh: torch.empty(*sh, dtype=self.tdt, device=self.dev)  # noqa: E731
+                b.update({"hn_lp": s(tokens, d), "big_lp": s(tokens, max(3 * d, 2 * f)), "att_lp": s(tokens, d),
+                          "gate_lp": s(tokens, d), "act_lp": s(tokens, f)})
+            self._bufs[key] = b
         return self._bufs[key]
 
     def forward_raw(self, tokens, key_valid, known, pos, group_start, group_end, role, covariates: bool, rows: int,
@@ -154,33 +175,54 @@ class HipTimestralModel:
         w = self.w
         ctx = chronos2.context(self.dev.index or 0)
         p = chronos2._ptr
+        lowp = self.code != _lib.JC_F32
         _lib.call("jc_ts_residual", ctx.handle, p(tokens), rows * enc, 2 * c.patch_size, p(w["embed_hidden_w"]),
                   p(w.get("embed_hidden_b")), p(w["embed_output_w"]), p(w.get("embed_output_b")),
                   p(w["embed_residual_w"]), p(w.get("embed_residual_b")), 4 * d, d, p(b["scratch"]), p(b["emb"]))
         _lib.call("jc_ts_assemble", ctx.handle, p(b["emb"]), p(w["query"]), p(b["x"]), rows, enc, n, d)
-        x, hn, big, att = b["x"], b["hn"], b["big"], b["att"]
-        # q|k|v and the MLP's up projection share one buffer, each a contiguous [tokens, width] view
-        qkv = big.view(-1)[: tokens_n * 3 * d].view(tokens_n, 3 * d)
-        up = big.view(-1)[: tokens_n * 2 * f].view(tokens_n, 2 * f)
+        x = b["x"]
+
+        def view(buf, width):  # a contiguous [tokens, width] view of a shared buffer
+            return buf.view(-1)[: tokens_n * width].view(tokens_n, width)
+
+        def norm(wt):  # the pre-norm, in the GEMM operands' type
+            if lowp:
+                chronos2.rms_norm_lp(x, wt, b["hn_lp"], c.norm_eps)
+                return b["hn_lp"]
+            chronos2.rms_norm(x, wt, b["hn"], c.norm_eps)
+            return b["hn"]
+
+        def gemm(a, wt, out, flags=0):
+            (chronos2.linear_lp if lowp else chronos2.linear)(a, wt, out, flags=flags)
+
         for lw in self.layers:
             for a in lw["attentions"]:
-                chronos2.rms_norm(x, a["norm"], hn, c.norm_eps)
-                chronos2.linear(hn, a["qkv"], qkv)
+                hn = norm(a["norm"])
+                # the time attention reads q|k|v and the gate in the storage type, the variate one in fp32
+                lp_att = lowp and a["time"]
+                qkv = view(b["big_lp"] if lp_att else b["big"], 3 * d)
+                att = b["att_lp"] if lp_att else b["att"]
+                gemm(hn, a["qkv"], qkv)
                 g = None
                 if a["gate"] is not None:
-                    chronos2.linear(hn, a["gate"], b["gate"])
-                    g = b["gate"]
+                    g = b["gate_lp"] if lp_att else b["gate"]
+                    gemm(hn, a["gate"], g)
                 if a["time"]:
                     timestral.time_attention(qkv, att, key_valid, known, pos, b["table"], g, rows, enc, ll, n, heads,
                                              dh, d)
                 else:
                     timestral.variate_attention(qkv, att, key_valid, group_start, group_end, role, covariates, g, rows,
                                                 enc, n, heads, dh, d)
-                chronos2.linear(att, a["wo"], x, flags=chronos2.GEMM_ACCUMULATE)
-            chronos2.rms_norm(x, lw["mlp_norm"], hn, c.norm_eps)
-            chronos2.linear(hn, lw["up"], up)
-            _lib.call("jc_swiglu", ctx.handle, p(up), p(b["act"]), tokens_n, f, _lib.JC_F32)
-            chronos2.linear(b["act"], lw["down"], x, flags=chronos2.GEMM_ACCUMULATE)
+                if lowp and not a["time"]:
+                    chronos2.to_lp(att, b["att_lp"])
+                    att = b["att_lp"]
+                gemm(att, a["wo"], x, chronos2.GEMM_ACCUMULATE)
+            hn = norm(lw["mlp_norm"])
+            up = view(b["big_lp"] if lowp else b["big"], 2 * f)
+            act = b["act_lp"] if lowp else b["act"]
+            gemm(hn, lw["up"], up)
+            _lib.call("jc_swiglu", ctx.handle, p(up), p(act), tokens_n, f, self.code)
+            gemm(act, lw["down"], x, chronos2.GEMM_ACCUMULATE)
         chronos2.rms_norm(x, w["out_norm"], b["y"], c.norm_eps)
         _lib.call("jc_ts_gather_decoder", ctx.handle, p(b["y"]), p(b["dec"]), rows, enc, n, h, d)
         _lib.call("jc_ts_residual", ctx.handle, p(b["dec"]), rows * h, d, p(w["head_hidden_w"]), None,

@@ -181,3 +181,30 @@ def test_predict_block_matches_oracle(gpu, oracle, covariates):
     print(f"  quantiles rel err {err:.3e}", flush=True)
     assert err <= 1e-3
     assert np.all(np.diff(got, axis=2) >= 0)  # non-crossing
+
+
+@pytest.mark.parametrize("dt", ["bf16", "fp16"])
+@pytest.mark.parametrize("name,c,rows,groups,enc,h,covariates", [CASES[0], CASES[2]], ids=["tiny", "d128"])
+def test_forward_lowp_matches_fp32_oracle(gpu, oracle, dt, name, c, rows, groups, enc, h, covariates):
+    """The FP16-GEMM mode (storage-type GEMM operands and time attention, fp32 accumulation and
+    residual stream) against the fp32 oracle on the same unrounded weights: within 2e-2."""
+    print(f"case ts forward {dt} {name}", flush=True)
+    ll = enc - h if covariates else enc
+    kv, known, position = cases.ts_layout(17, rows, enc, ll, h, known_frac=0.3 if covariates else 0.0)
+    per = rows // groups
+    group = np.repeat(np.arange(groups), per).astype(np.int32)
+    role = np.tile(np.array([0] + [1 + (i % 2) for i in range(per - 1)], np.int32), groups) if covariates \
+        else np.zeros(rows, np.int32)
+    w = tm.random_weights(c, seed=5, std=0.1)
+    r = np.random.default_rng(6)
+    tok = r.standard_normal((rows * enc, 2 * c.patch_size)).astype(np.float32)
+    model = tm.HipTimestralModel(c, w, dtype=dt)
+    gs, ge = chronos2.group_bounds(group)
+    raw = model.forward_raw(_t(tok), _i32(kv.reshape(-1)), _i32(known), _i32((position + enc).reshape(-1)), _i32(gs),
+                            _i32(ge), _i32(role) if covariates else None, covariates, rows, enc, h)
+    torch.cuda.synchronize()
+    exp = oracle.ts_forward_raw(tok, w, kv, known, position, group, role, covariates, rows, enc, ll, h, c.num_heads,
+                                c.head_dim, c.rope_dim, c.norm_eps, c.rope_theta)
+    err = oracle.rel_max_error(raw.cpu().numpy(), exp)
+    print(f"  raw rel err {err:.3e}", flush=True)
+    assert err <= 2e-2
