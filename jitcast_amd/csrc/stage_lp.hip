@@ -15,8 +15,8 @@
 // operands from LDS per 8 MFMAs. K advances 64 at a time through two LDS stages (A and W tiles of
 // 256 rows x 64 elements, 128 KB in all). The tiles arrive by direct-to-LDS buffer loads
 // (buffer_load_dwordx4 ... lds, 1 KB per wave instruction): a row of 64 elements is 8 chunks of
-// 16 bytes, and chunk c of row r sits at position c ^ (r & 7), so the MFMA operand reads (16 bytes
-// of 32 consecutive rows) hit distinct banks. Out-of-range rows and k columns read as zero through
+// 16 bytes, and chunk c of row r sits at position c ^ ((r >> 1) & 7), so the MFMA operand reads (16
+// bytes of 32 consecutive rows, 16 lanes per LDS cycle over 64 banks) hit distinct banks. Out-of-range rows and k columns read as zero through
 // the buffer descriptor's range check, so any m, n and k (a multiple of 8) need no clamping.
 // The grid is persistent (one workgroup per CU): a workgroup walks its tiles, and the first stage
 // of its next tile loads while the epilogue of the current one stores. Tiles that share a row
@@ -48,7 +48,10 @@ struct alignas(16) LpTile {  // 16-byte aligned, so operand reads stay ds_read_b
 };
 
 // element offset of chunk c (8 elements) of row r in a swizzled stage
-__device__ __forceinline__ int gswz(int r, int c) { return r * kBK + ((c ^ (r & 7)) << 3); }
+// chunk c of row r sits at position c ^ skey(r): rows r and r + 8 of a 16-lane read phase land in
+// different 16-byte bank groups
+__device__ __forceinline__ int skey(int r) { return (r >> 1) & 7; }
+__device__ __forceinline__ int gswz(int r, int c) { return r * kBK + ((c ^ skey(r)) << 3); }
 
 // raw buffer descriptor of `bytes` bytes at p (the base fits 48 bits, stride 0)
 __device__ __forceinline__ u32x4 buf_desc(const void* p, uint32_t bytes) {
@@ -128,14 +131,14 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_lp(const GemmLpArgs g, uint3
         const u32x4 ra = buf_desc(A + (size_t)m0 * g.lda, (uint32_t)min(kBM, g.m - m0) * a_row);
         const u32x4 rw = buf_desc(W + (size_t)n0 * g.k, (uint32_t)min(kBN, g.n - n0) * w_row);
         // recomputed per call from an opaque lane id, not hoisted into long-lived registers
-        const int ln = opaque(lane), srow = ln / 8, schunk = (ln % 8) ^ srow;
-        const int kc = st * kBK + 8 * schunk;
-        const bool kin = kc < g.k;
+        const int ln = opaque(lane), srow = ln / 8;
 #pragma unroll
         for (int u = u0; u < u1; u++) {
-            const uint32_t r = 8 * (kLoads * wave + u) + srow;
-            dma16(ra, kin ? r * a_row + 2u * kc : kOob, &lds.a[buf][8 * (kLoads * wave + u) * kBK]);
-            dma16(rw, kin ? r * w_row + 2u * kc : kOob, &lds.w[buf][8 * (kLoads * wave + u) * kBK]);
+            const int r = 8 * (kLoads * wave + u) + srow;
+            const int kc = st * kBK + 8 * ((ln % 8) ^ skey(r));  // the chunk this lane's position holds
+            const bool kin = kc < g.k;
+            dma16(ra, kin ? (uint32_t)r * a_row + 2u * kc : kOob, &lds.a[buf][8 * (kLoads * wave + u) * kBK]);
+            dma16(rw, kin ? (uint32_t)r * w_row + 2u * kc : kOob, &lds.w[buf][8 * (kLoads * wave + u) * kBK]);
         }
     };
 
