@@ -299,8 +299,9 @@ def ts_block_line(steps: int, warmup: int, dtype_name: str = "f32") -> dict:
     one forecast patch, 1024 tokens per series, a 123M-class model (d_model 768, 12 x 64, 12 layers
     of time + variate attention with gates, SwiGLU MLP 3072), random-init weights; fp32 or the
     FP16-GEMM mode in bf16.
-    value = series per second, wall clock around predict_block (host BlockLayout and BlockPrep, the
-    device forward, the host finish); the device forward alone timed with HIP events."""
+    value = series per second, wall clock around predict_block (BlockLayout's window on the host,
+    then BlockPrep, the forward and finish on the device, the quantiles copied back); the device
+    forward alone timed with HIP events."""
     import numpy as np
     import torch
 

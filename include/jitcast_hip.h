@@ -435,6 +435,31 @@ int jc_ts_gather_decoder(jc_ctx *ctx, const float *y, float *dec, int rows, int 
  */
 int jc_swiglu(jc_ctx *ctx, const void *up, void *act, int64_t tokens, int f, int dtype);
 
+/*
+ * The block's host ends on the device. jc_ts_prep = BlockPrep.of (J/timestral/BlockPrep.java:40-75)
+ * over the window of BlockLayout.of (J/timestral/BlockLayout.java:77-109): window [rows, w] fp32 and
+ * observed [rows, w] bytes (0 = missing), w = encoder tokens * patch, 1 <= patch <= 64; known [rows]
+ * int32 (nullable: no known rows) selects Scaler.instanceNorm (J/timestral/Scaler.java:87-110) over
+ * the causal patch scaler (Scaler.java:40-64). Writes tokens [rows * w/patch, 2*patch] (scaled values
+ * then missing flags), loc and scale [rows, w], and scaled [rows, w] (nullable). The double running
+ * sums keep the reference's step order.
+ */
+int jc_ts_prep(jc_ctx *ctx, const float *window, const uint8_t *observed, int rows, int w, int patch,
+               const int32_t *known, float minimum_scale, int use_asinh, float *tokens, float *scaled, float *loc,
+               float *scale);
+
+/*
+ * jc_ts_finish = BlockPrep.finish (J/timestral/BlockPrep.java:77-101): on raw [rows, h*patch, q]
+ * (the head's output), Quantiles.apply (J/timestral/Quantiles.java:52-77) with the per-level widths
+ * `width` (host memory, q floats: widthFactor * dp as Quantiles holds them) around level `median`,
+ * then Scaler.invert with loc / scale [rows, w] at step (context_patches - 1) * patch of each row and
+ * Scaler.clampNonFinite over each step's q values. out [rows, h*patch, q]; out == raw is allowed.
+ * q <= 32.
+ */
+int jc_ts_finish(jc_ctx *ctx, const float *raw, const float *loc, const float *scale, int rows, int w,
+                 int context_patches, int h, int patch, int q, const float *width, int median, int use_asinh,
+                 float *out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -85,6 +85,8 @@ SIGNATURES = {
     "jc_ts_assemble": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i]),
     "jc_ts_gather_decoder": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i]),
     "jc_swiglu": (_i, [_vp, _vp, _vp, _i64, _i, _i]),
+    "jc_ts_prep": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp, _f, _i, _vp, _vp, _vp, _vp]),
+    "jc_ts_finish": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp, _i, _i, _vp]),
     "jc_c2_prep": (_i, [_vp, _vp, _i64, _i, _vp, _i64, _i, _vp, _i, _i, _i, _i, _i, _f, _i, _vp, _vp, _vp, _vp]),
     "jc_c2_finish": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
     "jc_c2_residual": (_i, [_vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp]),

@@ -934,4 +934,37 @@ int jc_swiglu(jc_ctx* ctx, const void* up, void* act, int64_t tokens, int f, int
     return e == hipSuccess ? JC_OK : hip_fail(W, e);
 }
 
+int jc_ts_prep(jc_ctx* ctx, const float* window, const uint8_t* observed, int rows, int w, int patch,
+               const int32_t* known, float minimum_scale, int use_asinh, float* tokens, float* scaled, float* loc,
+               float* scale) {
+    const char* W = "jc_ts_prep";
+    int rc = use(ctx, W);
+    if (rc) return rc;
+    if (rows < 0 || w < 0 || patch < 1 || patch > 64 || w % patch)
+        return fail(JC_EINVAL, "%s: sizes (rows=%d w=%d patch=%d; 1 <= patch <= 64 dividing w)", W, rows, w, patch);
+    if ((int64_t)rows * w == 0) return JC_OK;
+    if (!window || !observed || !tokens || !loc || !scale) return fail(JC_EINVAL, "%s: null buffer", W);
+    hipError_t e = jc::ts_prep_launch(window, observed, rows, w, patch, known, minimum_scale, use_asinh, tokens, scaled,
+                                      loc, scale, ctx->stream);
+    return e == hipSuccess ? JC_OK : hip_fail(W, e);
+}
+
+int jc_ts_finish(jc_ctx* ctx, const float* raw, const float* loc, const float* scale, int rows, int w,
+                 int context_patches, int h, int patch, int q, const float* width, int median, int use_asinh,
+                 float* out) {
+    const char* W = "jc_ts_finish";
+    int rc = use(ctx, W);
+    if (rc) return rc;
+    if (rows < 0 || h < 1 || patch < 1 || q < 1 || q > jc::kTsMaxQuantiles || median < 0 || median >= q)
+        return fail(JC_EINVAL, "%s: sizes (rows=%d h=%d patch=%d q=%d median=%d; q <= %d)", W, rows, h, patch, q, median,
+                    jc::kTsMaxQuantiles);
+    if (context_patches < 1 || (int64_t)context_patches * patch > w)
+        return fail(JC_EINVAL, "%s: context_patches=%d * patch=%d exceeds the window w=%d", W, context_patches, patch, w);
+    if (rows == 0) return JC_OK;
+    if (!raw || !loc || !scale || !out || !width) return fail(JC_EINVAL, "%s: null buffer", W);
+    hipError_t e = jc::ts_finish_launch(raw, loc, scale, rows, w, (context_patches - 1) * patch, h * patch, q, width,
+                                        median, use_asinh, out, ctx->stream);
+    return e == hipSuccess ? JC_OK : hip_fail(W, e);
+}
+
 }  // extern "C"

@@ -103,4 +103,12 @@ hipError_t c2_prep_launch(const float* ctx, int64_t ld_ctx, int steps, const flo
 hipError_t c2_finish_launch(const float* raw, const float* loc, const float* scale, const int32_t* order, int rows,
                             int h, int q, int patch, int arcsinh, float* out, hipStream_t stream);
 
+constexpr int kTsMaxQuantiles = 32;
+hipError_t ts_prep_launch(const float* window, const uint8_t* observed, int rows, int w, int patch,
+                          const int32_t* known, float minimum_scale, int use_asinh, float* tok, float* scaled,
+                          float* loc, float* scale, hipStream_t stream);
+hipError_t ts_finish_launch(const float* raw, const float* loc, const float* scale, int rows, int w, int anchor,
+                            int steps, int q, const float* width, int median, int use_asinh, float* out,
+                            hipStream_t stream);
+
 }  // namespace jc

@@ -14,14 +14,16 @@ TimestralForward.java:327-382).
                       jc_swiglu, jc_linear accumulated), the output norm, the decoder tokens
                       (jc_ts_gather_decoder) and the head (jc_ts_residual)
 
-  block_window, block_prep, quantile_map, block_finish
-                      the host ends of predict_block, numpy restatements with the reference's
-                      float/double rounding: BlockLayout.of's window (J/timestral/BlockLayout.java
-                      :77-148), BlockPrep.of (BlockPrep.java:40-75; Scaler.java's causal patch
-                      loc/scale, instance norm, affine), Quantiles.apply (Quantiles.java:52-77) and
-                      BlockPrep.finish (BlockPrep.java:77-101; Scaler.invert, clampNonFinite)
+  block_window        BlockLayout.of's window (J/timestral/BlockLayout.java:77-148) on the host
+  block_prep, quantile_map, block_finish
+                      numpy restatements of BlockPrep.of (BlockPrep.java:40-75; Scaler.java's causal
+                      patch loc/scale, instance norm, affine), Quantiles.apply (Quantiles.java:52-77)
+                      and BlockPrep.finish (BlockPrep.java:77-101; Scaler.invert, clampNonFinite),
+                      with the reference's float/double rounding, for callers that hold the block on
+                      the host; predict_block runs the device versions (jc_ts_prep, jc_ts_finish)
   HipTimestralModel.predict_block
-                      BlockLayout + BlockPrep on the host, the device forward, finish on the host
+                      the window and BlockLayout on the host, then BlockPrep, the forward and finish
+                      on the device
 """
 from __future__ import annotations
 
@@ -232,28 +234,45 @@ class HipTimestralModel:
 
     def predict_block(self, inputs, observed, group, h: int, role=None, known_future=None, known_future_mask=None):
         """TimestralModel.predict_block on one block, as CpuTimestral.predictBlock runs it
-        (J/timestral/cpu/CpuTimestral.java:127-188): BlockLayout (jc_ts_block_layout) and BlockPrep
-        on the host, the device forward, BlockPrep.finish on the host. inputs / observed [rows, t]
-        (t a multiple of the patch), group [rows] with each series' rows contiguous, h forecast
-        patches, role [rows] (0 TARGET, 1 PAST, 2 KNOWN) and the known covariates' future steps
-        [rows, h*P] for a covariate block. Returns [rows, h*P, Q] quantiles."""
+        (J/timestral/cpu/CpuTimestral.java:127-188): BlockLayout's window and masks on the host
+        (block_window, jc_ts_block_layout), then on the device BlockPrep (jc_ts_prep), the forward and
+        BlockPrep.finish (jc_ts_finish), so only the window goes up and the quantiles come down.
+        inputs / observed [rows, t] (t a multiple of the patch), group [rows] with each series' rows
+        contiguous, h forecast patches, role [rows] (0 TARGET, 1 PAST, 2 KNOWN) and the known
+        covariates' future steps [rows, h*P] for a covariate block. Returns [rows, h*P, Q]
+        quantiles."""
         import torch
 
         c = self.c
-        ps = c.patch_size
+        ps, q = c.patch_size, c.num_quantiles
         window, obs, cov = block_window(c, inputs, observed, role, known_future, known_future_mask, h)
         rows, t = np.asarray(inputs).shape
+        wlen = window.shape[1]
         enc, cov_l, kv, known, pos = timestral.block_layout(
             observed, group, h, ps, role=role if cov else None, future_observed=known_future_mask if cov else None,
             covariate_enabled=c.covariate_enabled, attend_missing=c.attend_missing, block_size=c.block_size)
-        if enc != window.shape[1] // ps or cov_l != cov:
+        if enc != wlen // ps or cov_l != cov:
             raise _lib.JitcastError(_lib.JC_EINVAL, "block layout and window disagree")
-        tok, _, loc, scale = block_prep(c, window, obs, known)
         gs, ge = chronos2.group_bounds(group)
-        up = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.int32)).to(self.dev)  # noqa: E731
-        raw = self.forward_raw(torch.from_numpy(tok).to(self.dev), up(kv.reshape(-1)), up(known), up(pos.reshape(-1)),
-                               up(gs), up(ge), up(role) if cov else None, cov, rows, enc, h)
-        return block_finish(c, raw.cpu().numpy(), loc, scale, t // ps, h)
+        dev = self.dev
+        up = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.int32)).to(dev)  # noqa: E731
+        ctx = chronos2.context(dev.index or 0)
+        p = chronos2._ptr
+        win_d = torch.from_numpy(np.ascontiguousarray(window, np.float32)).to(dev)
+        obs_d = torch.from_numpy(np.ascontiguousarray(obs, np.uint8)).to(dev)
+        known_d = up(known)
+        tok = torch.empty(rows * enc, 2 * ps, dtype=torch.float32, device=dev)
+        loc = torch.empty(rows, wlen, dtype=torch.float32, device=dev)
+        scale = torch.empty(rows, wlen, dtype=torch.float32, device=dev)
+        _lib.call("jc_ts_prep", ctx.handle, p(win_d), p(obs_d), rows, wlen, ps, p(known_d), c.minimum_scale,
+                  int(c.use_asinh), p(tok), None, p(loc), p(scale))
+        raw = self.forward_raw(tok, up(kv.reshape(-1)), known_d, up(pos.reshape(-1)), up(gs), up(ge),
+                               up(role) if cov else None, cov, rows, enc, h)
+        out = torch.empty(rows, h * ps, q, dtype=torch.float32, device=dev)
+        widths = quantile_widths(c)
+        _lib.call("jc_ts_finish", ctx.handle, p(raw), p(loc), p(scale), rows, wlen, t // ps, h, ps, q,
+                  widths.ctypes.data, c.median_index, int(c.use_asinh), p(out))
+        return out.cpu().numpy()
 
 
 FLOAT32_EPS = np.float32(np.finfo(np.float32).eps)
@@ -359,18 +378,24 @@ def _softplus(x):
     return np.where(x > 20, x, np.log1p(np.exp(np.minimum(xd, 20.0))).astype(np.float32)).astype(np.float32)
 
 
+def quantile_widths(c: TimestralConfig):
+    """Quantiles' per-level widthFactor * dp (Quantiles.java:30-41): the gap to the next level inward,
+    rounded to float, times the float width factor. float32 [Q]."""
+    knots = np.asarray(c.quantiles, np.float64)
+    q, med = len(knots), c.median_index
+    width = np.zeros(q, np.float32)
+    for i in range(q):
+        width[i] = np.float32(knots[i] - knots[i - 1] if i > med else knots[i + 1] - knots[i] if i < med else 0.0)
+    return (np.float32(c.quantile_width_factor) * width).astype(np.float32)
+
+
 def quantile_map(c: TimestralConfig, raw):
     """Quantiles.apply (Quantiles.java:52-77) on every row of raw [..., Q]: the median kept, each
     level above it the median plus the running sum of widthFactor*dp*softplus(raw), each level
     below minus it, clamped to the finite float range. Widths rounded to float as the reference's
     tensor holds them."""
-    knots = np.asarray(c.quantiles, np.float64)
-    q = len(knots)
-    med = c.median_index
-    width = np.zeros(q, np.float32)
-    for i in range(q):
-        width[i] = np.float32(knots[i] - knots[i - 1] if i > med else knots[i + 1] - knots[i] if i < med else 0.0)
-    width = (np.float32(c.quantile_width_factor) * width).astype(np.float32)
+    q, med = c.num_quantiles, c.median_index
+    width = quantile_widths(c)
     raw = np.asarray(raw, np.float32)
     out = np.empty_like(raw)
     m = raw[..., med]
