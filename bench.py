@@ -244,8 +244,11 @@ def ts_time_attention_line(steps: int, warmup: int) -> dict:
 def forecast_line(steps: int, warmup: int, dtype_name: str = "f32") -> dict:
     """Config 4 end to end: HipChronos2Model.forecast on 1024 groups x (4 series + 1 known-future
     covariate) of 2048 steps, horizon 64, 21 quantiles, Chronos-2 120M-class random-init weights.
-    value = target series forecast per second, wall clock around forecast() (host layout and prep,
-    one upload, the device forward, one download, the inverse norm)."""
+    value = target series forecast per second, wall clock around forecast() (the group order on the
+    host, one upload, jc_c2_prep, the device forward launched kernel by kernel, jc_c2_finish, one
+    download). The same forecast with the forward replayed from its plan (max_plans: one hipGraph
+    per shape, as the reference's forward runs from its PlanCache) is timed beside it, at config 4
+    and on a 20-row request."""
     import numpy as np
     import torch
 
@@ -254,17 +257,39 @@ def forecast_line(steps: int, warmup: int, dtype_name: str = "f32") -> dict:
     c = cm.Chronos2Config()  # d_model 768, 12 x 64, 12 layers, d_ff 3072, patch 16, 21 quantiles
     w = cm.random_weights(c, seed=0)
     model = cm.HipChronos2Model(c, w, dtype=dtype_name)
+    planned = cm.HipChronos2Model(c, w, dtype=dtype_name, max_plans=1)
     del w
     ctx, group, fut, targets = synthetic.c2_forecast_config4()
     h = 64 // c.patch_size
-    for _ in range(warmup):
-        model.forecast(ctx, group, fut, h=h)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        out = model.forecast(ctx, group, fut, h=h)
-    torch.cuda.synchronize()
-    wall = (time.perf_counter() - t0) / steps
+
+    def timed(m):
+        for _ in range(warmup):
+            m.forecast(ctx, group, fut, h=h)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            o = m.forecast(ctx, group, fut, h=h)
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / steps, o
+
+    wall, out = timed(model)
+    plan_wall, plan_out = timed(planned)
+    assert np.array_equal(out, plan_out)
+    # a small request (4 groups = 20 rows, 512 steps), where launching ~200 kernels from the host
+    # costs more than the device work
+    small = (ctx[:20, -512:], group[:20], fut[:20] if fut is not None else None)
+    lat = {}
+    for name, m in (("eager", model), ("plan", planned)):
+        for _ in range(3):
+            m.forecast(*small, h=h)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(20):
+            m.forecast(*small, h=h)
+        torch.cuda.synchronize()
+        lat[name] = (time.perf_counter() - t0) / 20 * 1e3
+    planned.close()
+    del planned
     # the device forward alone (prepared tokens resident), HIP events
     lay = cm.layout(c, ctx, group, fut, h)
     tok, _, _ = cm.prep(c, lay)
@@ -275,8 +300,10 @@ def forecast_line(steps: int, warmup: int, dtype_name: str = "f32") -> dict:
     dev_ms = time_launches(lambda: model.forward_raw(*args), max(2, steps), 1)
     series = int(targets.sum())
     assert np.isfinite(out).all()
-    log(f"forecast {dtype_name}: {wall * 1e3:.1f} ms per call end to end ({series / wall:.0f} series/s), device "
-        f"forward {dev_ms:.1f} ms ({series / (dev_ms * 1e-3):.0f} series/s)")
+    log(f"forecast {dtype_name}: {wall * 1e3:.1f} ms per call end to end ({series / wall:.0f} series/s; from the "
+        f"plan {plan_wall * 1e3:.1f} ms, {series / plan_wall:.0f} series/s), device forward "
+        f"{dev_ms:.1f} ms ({series / (dev_ms * 1e-3):.0f} series/s); 20-row request {lat['plan']:.2f} ms from the "
+        f"plan, {lat['eager']:.2f} ms eager")
     res = {
         "workload": f"config 4: Chronos-2 120M-class forecast ({dtype_name} encoder), 1024 groups x (4 series + 1 "
                     "known-future covariate) x 2048 steps, horizon 64, 21 quantiles, random-init weights",
@@ -284,6 +311,9 @@ def forecast_line(steps: int, warmup: int, dtype_name: str = "f32") -> dict:
         "value": round(series / wall, 1),
         "unit": "series/s",
         "ms_per_call": round(wall * 1e3, 2),
+        "plan_ms_per_call": round(plan_wall * 1e3, 2),
+        "plan_series_per_s": round(series / plan_wall, 1),
+        "small_request_ms": {"rows": 20, "steps": 512, "plan": round(lat["plan"], 3), "eager": round(lat["eager"], 3)},
         "device_forward_ms": round(dev_ms, 2),
         "device_series_per_s": round(series / (dev_ms * 1e-3), 1),
         "rows": lay.rows, "tokens_per_row": lay.n,

@@ -25,6 +25,7 @@ from dataclasses import dataclass, field
 import numpy as np
 
 from . import _lib, chronos2
+from . import plans as plans_mod
 
 QUANTILES_21 = (0.01, 0.05, 0.1, 0.15, 0.2, 0.25, 0.3, 0.35, 0.4, 0.45, 0.5, 0.55, 0.6, 0.65, 0.7, 0.75, 0.8, 0.85,
                 0.9, 0.95, 0.99)
@@ -196,7 +197,13 @@ class HipChronos2Model:
     "bf16"/"fp16" runs the encoder layers' GEMMs and time attention in that type with fp32
     accumulation (the reference's FP16 GEMM mode), the embeddings and head in fp32."""
 
-    def __init__(self, c: Chronos2Config, weights: dict, dtype: str = "f32", device: int = 0):
+    def __init__(self, c: Chronos2Config, weights: dict, dtype: str = "f32", device: int = 0, max_plans: int = 0,
+                 plan_bytes: int | None = None):
+        """max_plans > 0 runs the device forward as captured plans, one hipGraph per
+        Shape(rows, contextPatches, outputPatches) (Chronos2Forward.Shape, Chronos2Forward.java:106),
+        kept in a PlanCache of at most max_plans plans within plan_bytes of plan buffers
+        (Chronos2Forward.java:108-113; default: no byte limit). The weights are uploaded once and
+        shared by every plan, so a plan's footprint is its shape's buffers only."""
         import torch
 
         self.c, self.dtype = c, dtype
@@ -216,32 +223,47 @@ class HipChronos2Model:
                     d[k] = lp
             self.layers.append(d)
         self._bufs = {}
+        self.plans = None
+        if max_plans > 0:
+            self.plans = plans_mod.PlanCache(max_plans, plan_bytes if plan_bytes else 1 << 62)
+            self._stream = torch.cuda.Stream(self.dev)  # default priority; plans capture and replay on it
 
-    def _buffers(self, rows: int, nc: int, h: int):
+    def _alloc(self, rows: int, nc: int, h: int, inputs: bool = False) -> dict:
+        """One shape's device buffers (Chronos2Forward.Plan's, Chronos2Forward.java:206-236); with
+        inputs, also the forward's inputs (tokens, live, group bounds) that a plan replays from."""
         import torch
 
+        c = self.c
+        nreg = 1 if c.use_reg_token else 0
+        n = nc + nreg + h
+        ne, d, ff = nc + h, c.d_model, c.d_ff
+        f = lambda *s: torch.empty(*s, dtype=torch.float32, device=self.dev)  # noqa: E731
+        ws = chronos2.layer_workspace_bytes(rows, n, d, c.inner, ff, self.code)
+        b = {
+            "emb": f(rows * ne, d), "scratch": f(rows * max(ne, h), ff), "x": f(rows * n, d),
+            "y": f(rows * n, d), "dec": f(rows * h, d), "raw": f(rows * h, c.num_quantiles * c.patch_size),
+            "ws": f(ws // 4 + 64), "table": torch.from_numpy(chronos2.rope_table(n, c.d_kv, c.rope_theta)).to(self.dev),
+        }
+        if inputs:
+            i32 = lambda m: torch.empty(m, dtype=torch.int32, device=self.dev)  # noqa: E731
+            b.update({"tok": f(rows * ne, 3 * c.patch_size), "live": i32(rows * n), "gs": i32(rows), "ge": i32(rows)})
+        return b
+
+    def _buffers(self, rows: int, nc: int, h: int):
         key = (rows, nc, h)
         if key not in self._bufs:
-            self._bufs.clear()  # one shape at a time, as a plan per shape would hold them
-            c = self.c
-            n = nc + (1 if c.use_reg_token else 0) + h
-            ne, d, ff = nc + h, c.d_model, c.d_ff
-            f = lambda *s: torch.empty(*s, dtype=torch.float32, device=self.dev)  # noqa: E731
-            ws = chronos2.layer_workspace_bytes(rows, n, d, c.inner, ff, self.code)
-            self._bufs[key] = {
-                "emb": f(rows * ne, d), "scratch": f(rows * max(ne, h), ff), "x": f(rows * n, d),
-                "y": f(rows * n, d), "dec": f(rows * h, d), "raw": f(rows * h, c.num_quantiles * c.patch_size),
-                "ws": f(ws // 4 + 64), "table": torch.from_numpy(chronos2.rope_table(n, c.d_kv, c.rope_theta)).to(self.dev),
-            }
+            self._bufs.clear()  # the eager forward keeps one shape's buffers
+            self._bufs[key] = self._alloc(rows, nc, h)
         return self._bufs[key]
 
-    def forward_raw(self, tokens, live, group_start, group_end, rows: int, nc: int, h: int):
+    def forward_raw(self, tokens, live, group_start, group_end, rows: int, nc: int, h: int, bufs: dict | None = None):
         """The device forward from prepared tokens (torch [rows*(nc+h), 3P] on the GPU) to the raw
-        output patch embedding [rows*h, Q*P] on the GPU; rows grouped contiguously."""
+        output patch embedding [rows*h, Q*P] on the GPU; rows grouped contiguously. bufs: a plan's
+        buffers (default: the eager forward's)."""
         c = self.c
         nreg = 1 if c.use_reg_token else 0
         n, ne, d, ff = nc + nreg + h, nc + h, c.d_model, c.d_ff
-        b = self._buffers(rows, nc, h)
+        b = bufs if bufs is not None else self._buffers(rows, nc, h)
         w = self.w
         ctx = chronos2.context(self.dev.index or 0)
         p = chronos2._ptr
@@ -275,6 +297,9 @@ class HipChronos2Model:
         up = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
         ord_t = up(order) if order is not None else None
         nreg = 1 if c.use_reg_token else 0
+        if self.plans is not None:
+            with torch.cuda.stream(self._stream):
+                return self._forecast_planned(ctx, fut, order, gs, ge, rows, h)
         tok, loc, scale, live, nc = chronos2.prep(up(ctx), up(fut) if fut is not None else None, ord_t, rows,
                                                   c.context_length, c.patch_size, h, nreg, c.time_encoding_scale,
                                                   c.use_arcsinh)
@@ -282,6 +307,67 @@ class HipChronos2Model:
         out = torch.empty(rows, c.num_quantiles, h * c.patch_size, dtype=torch.float32, device=dev)
         chronos2.finish(raw, loc, scale, ord_t, rows, h, c.num_quantiles, c.patch_size, c.use_arcsinh, out)
         return out.cpu().numpy()
+
+    def _forecast_planned(self, ctx, fut, order, gs, ge, rows: int, h: int) -> np.ndarray:
+        """forecast through the plan of its shape (Chronos2Forward.forward's plans.run): the
+        uploads and jc_c2_prep, then the plan's forward replayed on its own buffers (captured on the
+        shape's first use), then jc_c2_finish. Runs on the model's stream."""
+        import torch
+
+        c = self.c
+        dev = self.dev
+        up = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+        ord_t = up(order) if order is not None else None
+        nreg = 1 if c.use_reg_token else 0
+        tok, loc, scale, live, nc = chronos2.prep(up(ctx), up(fut) if fut is not None else None, ord_t, rows,
+                                                  c.context_length, c.patch_size, h, nreg, c.time_encoding_scale,
+                                                  c.use_arcsinh)
+        shape = (rows, nc, h)
+
+        def use(plan: ShapePlan):
+            b = plan.bufs
+            b["tok"].copy_(tok)
+            b["live"].copy_(live)
+            b["gs"].copy_(up(gs))
+            b["ge"].copy_(up(ge))
+            plan.graph.launch()
+            out = torch.empty(rows, c.num_quantiles, h * c.patch_size, dtype=torch.float32, device=dev)
+            chronos2.finish(b["raw"], loc, scale, ord_t, rows, h, c.num_quantiles, c.patch_size, c.use_arcsinh, out)
+            return out.cpu().numpy()
+
+        return self.plans.run(shape, self._capture, use)
+
+    def _capture(self, shape) -> "ShapePlan":
+        """Chronos2Forward.Plan's constructor: the shape's buffers, then the device forward captured
+        into one hipGraph on the model's stream (nothing allocates while it captures)."""
+        import torch
+
+        rows, nc, h = shape
+        b = self._alloc(rows, nc, h, inputs=True)
+        with torch.cuda.stream(self._stream):
+            with plans_mod.capture((rows << 40) | (nc << 20) | h, self.dev.index or 0) as box:
+                self.forward_raw(b["tok"], b["live"], b["gs"], b["ge"], rows, nc, h, bufs=b)
+        return ShapePlan(box[0], b)
+
+    def close(self) -> None:
+        """Closes every cached plan (Chronos2Forward.close)."""
+        if self.plans is not None:
+            self.plans.close()
+
+
+class ShapePlan:
+    """One shape's captured forward and the buffers it replays on (PlanCache.Plan): its footprint
+    is those buffers plus what the graph adopted; the weights are not counted, being shared."""
+
+    def __init__(self, graph, bufs: dict):
+        self.graph, self.bufs = graph, bufs
+
+    def device_bytes(self) -> int:
+        return self.graph.device_bytes() + sum(t.numel() * t.element_size() for t in self.bufs.values())
+
+    def close(self) -> None:
+        self.graph.close()
+        self.bufs = {}
 
 
 def _check_inputs(c: Chronos2Config, context, group, future_covariates, h: int):

@@ -85,3 +85,35 @@ def test_forecast_lowp_encoder(gpu, oracle, dt):
     err = oracle.rel_max_error(got, exp)
     print(f"{dt} encoder forecast rel err {err:.3e}", flush=True)
     assert err <= 2e-2
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_planned_forecast_matches_eager(gpu, dt):
+    """HipChronos2Model with max_plans: the device forward captured once per
+    Shape(rows, contextPatches, outputPatches) and replayed (Chronos2Forward.java:106, PlanCache.run).
+    Every replay, with fresh inputs and eager work between replays, equals the eager forecast bit for
+    bit; a third shape evicts the least recently used plan; the weights are not part of any plan's
+    bytes."""
+    print(f"case planned forecast {dt}", flush=True)
+    c = SMALL
+    w = cm.random_weights(c, seed=3, std=0.1)
+    eager = cm.HipChronos2Model(c, w, dtype=dt)
+    planned = cm.HipChronos2Model(c, w, dtype=dt, max_plans=2)
+    try:
+        # (rows, steps, groups, h): three shapes, the first one again after the second
+        runs = [(6, 200, [0, 0, 1, 1, 1, 2], 2), (4, 96, [0, 1, 1, 2], 1), (6, 200, [0, 1, 1, 2, 2, 2], 2),
+                (3, 256, [0, 0, 0], 3), (6, 200, [2, 2, 1, 0, 0, 1], 2)]
+        for k, (rows, steps, group, h) in enumerate(runs):
+            ctx = _context(10 + k, rows, steps, lead_nan=[(17 * k + 5 * i) % steps for i in range(rows)])
+            got = planned.forecast(ctx, group, None, h=h)
+            exp = eager.forecast(ctx, group, None, h=h)
+            torch.cuda.synchronize()
+            np.testing.assert_array_equal(got, exp)
+        nc = lambda steps: (min(steps, c.context_length) + c.patch_size - 1) // c.patch_size  # noqa: E731
+        # shapes A = (6, 200, 2), B = (4, 96, 1), C = (3, 256, 3): A, B, A (hit), C evicts B, A (hit)
+        assert planned.plans.keys() == [(3, nc(256), 3), (6, nc(200), 2)]
+        weights = sum(t.numel() * t.element_size() for t in planned.w.values())
+        assert 0 < planned.plans.cached_bytes() < 2 * weights + (64 << 20)
+    finally:
+        planned.close()
+    assert planned.plans.keys() == []
