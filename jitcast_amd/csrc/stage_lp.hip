@@ -176,21 +176,29 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_lp(const GemmLpArgs g, uint3
             lds_barrier();
             // the next stage's loads are spread over the first two k-steps, so the per-CU address
             // unit works through them while the MFMAs run instead of stalling every wave at once
+            // operands of k-step kk sit in registers set kk % 2: the next k-step's LDS reads are
+            // issued before this k-step's MFMAs (the scheduling barrier keeps them there), so their
+            // latency runs under 8 MFMAs instead of stalling the first one
+            x8 av[2][kTM], wv[2][kTN];
+            auto operands = [&](int kk, int s) __attribute__((always_inline)) {
+                const int c = 2 * kk + hg;
+#pragma unroll
+                for (int ti = 0; ti < kTM; ti++)
+                    av[s][ti] = __builtin_bit_cast(x8, *reinterpret_cast<const u32x4*>(&lds.a[buf][gswz(128 * wm + 32 * ti + j, c)]));
+#pragma unroll
+                for (int tj = 0; tj < kTN; tj++)
+                    wv[s][tj] = __builtin_bit_cast(x8, *reinterpret_cast<const u32x4*>(&lds.w[buf][gswz(64 * wn + 32 * tj + j, c)]));
+            };
+            operands(0, 0);
 #pragma unroll
             for (int kk = 0; kk < kBK / 16; kk++) {
                 if (kk < 2 && st + 1 < stages) issue(tile, st + 1, buf ^ 1, 0, kk * kLoads / 2, (kk + 1) * kLoads / 2);
-                const int c = 2 * kk + hg;
-                x8 av[kTM], wv[kTN];
-#pragma unroll
-                for (int ti = 0; ti < kTM; ti++)
-                    av[ti] = __builtin_bit_cast(x8, *reinterpret_cast<const u32x4*>(&lds.a[buf][gswz(128 * wm + 32 * ti + j, c)]));
-#pragma unroll
-                for (int tj = 0; tj < kTN; tj++)
-                    wv[tj] = __builtin_bit_cast(x8, *reinterpret_cast<const u32x4*>(&lds.w[buf][gswz(64 * wn + 32 * tj + j, c)]));
+                if (kk + 1 < kBK / 16) operands(kk + 1, (kk + 1) & 1);
+                __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int ti = 0; ti < kTM; ti++)
 #pragma unroll
-                    for (int tj = 0; tj < kTN; tj++) acc[ti][tj] = Lp<T>::mfma(av[ti], wv[tj], acc[ti][tj]);
+                    for (int tj = 0; tj < kTN; tj++) acc[ti][tj] = Lp<T>::mfma(av[kk & 1][ti], wv[kk & 1][tj], acc[ti][tj]);
             }
         }
         // every wave is done with both stages: the next tile's first stage may load
