@@ -389,7 +389,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=256)
-    ap.add_argument("--only", choices=["all", "time", "group", "bf16", "fp16", "layer", "layer-bf16", "ts", "ts-block", "forecast"], default="all",
+    ap.add_argument("--only", choices=["all", "time", "group", "bf16", "fp16", "layer", "layer-bf16", "ts", "ts-block", "ts-block-bf16", "forecast"], default="all",
                     help="which workloads to run (profiling runs select one kernel)")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="only run 5 plain device copies of this many bytes (calibrates rocprof byte counters)")
@@ -422,10 +422,10 @@ def main() -> int:
         if args.only == "forecast":
             print(json.dumps({"also": also}), flush=True)
             return 0
-    if args.only in ("all", "ts-block"):
-        for name in ("bf16", "f32"):
+    if args.only in ("all", "ts-block", "ts-block-bf16"):
+        for name in (("bf16",) if args.only == "ts-block-bf16" else ("bf16", "f32")):
             also[f"ts_block_{name}"] = ts_block_line(2, 1, name)
-        if args.only == "ts-block":
+        if args.only in ("ts-block", "ts-block-bf16"):
             print(json.dumps({"also": also}), flush=True)
             return 0
     if args.only in ("all", "ts"):

@@ -79,9 +79,50 @@ __global__ __launch_bounds__(kWave) void group_attention_f32(const GroupArgs a, 
     const bool enc_slot = TS && t < a.enc;
     const bool cov = TS && a.covariates != 0 && a.role != nullptr;
 
-    // the groups starting in this tile
-    const uint32_t starts = (uint32_t)__ballot(lane < nr && a.gstart[r0 + lane] == r0 + lane) & 0xffffu;
+    // the groups starting in this tile (both bounds loaded at once: one round trip)
+    const int gs_l = lane < nr ? a.gstart[r0 + lane] : -1;
+    const int ge_l = lane < nr ? a.gend[r0 + lane] : 0;
+    const uint32_t starts = (uint32_t)__ballot(gs_l == r0 + lane) & 0xffffu;
     if (starts == 0) return;
+
+    // A tile of one-row groups (every series of the block univariate): a row's only key is itself,
+    // so its softmax weight is exactly 1 for a finite score and its output is its own v (gated),
+    // which a stream over (row, head) pairs writes without MFMA work. The outcomes are the job
+    // stream's below: 0 where the row may not read itself (Chronos-2: its token is not live) or its
+    // score is -inf, NaN where the score is NaN or +inf, v otherwise.
+    const bool single = lane >= nr || (gs_l == r0 + lane && (ge_l <= r0 + lane + 1 || r0 + lane + 1 >= rows));
+    if (__ballot(!single) == 0) {
+        const int pj = lane % 16;  // 16 lanes per (row, head) pair, 4 dims each per 64-dim step
+        for (int pr = lane / 16; pr < nr * heads; pr += kWave / 16) {
+            const int row = r0 + pr / heads, h = pr % heads;
+            const float* tokp = qkv + ((size_t)row * tok_n + t) * stride + h * dh;
+            float sc = 0.f;
+            for (int e = 4 * pj; e < dh; e += 64) {
+                const floatx4 q4 = *reinterpret_cast<const floatx4*>(tokp + e);
+                const floatx4 k4 = *reinterpret_cast<const floatx4*>(tokp + inner + e);
+#pragma unroll
+                for (int u = 0; u < 4; u++) sc += (q4[u] * a.qscale) * k4[u];
+            }
+#pragma unroll
+            for (int o = 8; o > 0; o >>= 1) sc += __shfl_xor(sc, o, 16);
+            const bool self_ok = TS || a.valid[(size_t)row * tok_n + t] != 0;
+            const bool zero = !self_ok || sc == -INFINITY;
+            const bool nan = !zero && !(sc < INFINITY);  // NaN or +inf
+            const size_t off = ((size_t)row * tok_n + t) * inner + h * dh;
+            for (int e = 4 * pj; e < dh; e += 64) {
+                floatx4 v = *reinterpret_cast<const floatx4*>(tokp + 2 * inner + e);
+#pragma unroll
+                for (int u = 0; u < 4; u++) v[u] = zero ? 0.f : nan ? __builtin_nanf("") : v[u];
+                if (a.gate) {
+                    const floatx4 gv = *reinterpret_cast<const floatx4*>(a.gate + off + e);
+#pragma unroll
+                    for (int u = 0; u < 4; u++) v[u] *= 1.f / (1.f + fast_exp2(-gv[u] * kLog2e));
+                }
+                *reinterpret_cast<floatx4*>(a.out + off + e) = v;
+            }
+        }
+        return;
+    }
 
     auto first_of = [&](uint32_t rest) {
         Job jb;

@@ -31,6 +31,8 @@ CASES = [
     (50, 3, 4, 16, 64, 5, 5, 0.7),
     (33, 2, 2, 48, 100, 3, 20, 0.6),
     (17, 1, 1, 64, 64, 17, 17, 1.0),
+    (48, 5, 12, 64, 768, 1, 1, 0.7),  # one-row groups: the streaming path
+    (21, 3, 2, 16, 32, 1, 1, 0.5),
 ]
 
 
@@ -69,3 +71,13 @@ def test_fp32_config2_shape_subset(gpu, oracle):
     err = oracle.rel_max_error(got, exp)
     print(f"config-2 subset rel err {err:.3e}", flush=True)
     assert err <= TOL_F32
+
+
+def test_one_row_groups_output_v_or_zeros(gpu):
+    """A one-row group reads only itself: v where its token is live, zeros where it is not."""
+    rows, n, heads, dh, inner = 40, 6, 12, 64, 768
+    qkv = cases.qkv(45, rows * n, inner)
+    live = cases.random_live(45, rows, n, 0.6)
+    got = _run(qkv, live, np.arange(rows, dtype=np.int32), rows, n, heads, dh, inner)
+    exp = np.where(live.reshape(-1, 1) != 0, qkv[:, 2 * inner:], np.float32(0))
+    np.testing.assert_array_equal(got, exp)

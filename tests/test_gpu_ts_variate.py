@@ -42,6 +42,12 @@ CASES = [
     (20, 3, 1, 1, 128, 128, 20, 20, 1, 0.6, True),  # 128-wide heads
     (17, 2, 0, 2, 48, 96, 17, 17, 0, 1.0, False),
     (40, 0, 3, 2, 64, 128, 2, 9, 1, 1.0, False),  # decoder slots only
+    # one-row groups (univariate series) take the streaming path per 16-row tile
+    (80, 7, 2, 12, 64, 768, 1, 1, 1, 0.6, True),
+    (21, 3, 1, 2, 128, 256, 1, 1, 0, 0.7, False),
+    (19, 2, 2, 3, 24, 72, 1, 1, 0, 0.5, True),
+    (35, 3, 1, 2, 48, 96, 1, 1, 1, 0.8, False),
+    (70, 3, 1, 2, 64, 128, 1, 2, 0, 0.7, True),  # tiles of singletons beside mixed tiles
 ]
 
 
@@ -91,3 +97,15 @@ def test_bf16_is_not_built_yet(gpu):
     z = torch.zeros(4, dtype=torch.int32, device=dev)
     with pytest.raises(JitcastError, match="not built"):
         timestral.variate_attention(q, o, z, z, z + 1, None, False, None, 4, 1, 1, 1, 64, 64)
+
+
+def test_univariate_rows_output_their_own_v(gpu):
+    """A one-row group's only key is the row itself (always allowed, BlockLayout.java:228-230): its
+    softmax weight is 1, so the output is its own v bit for bit, whatever the key validity."""
+    rows, enc, h, heads, dh, d = 40, 5, 2, 12, 64, 768
+    n = enc + h
+    qkv = cases.qkv(111, rows * n, d)
+    kv = cases.random_live(111, rows, enc, 0.5)
+    group = np.arange(rows, dtype=np.int32)
+    got = _run(qkv, kv, group, np.zeros(rows, np.int32), 0, None, rows, enc, n, heads, dh, d)
+    np.testing.assert_array_equal(got, qkv[:, 2 * d:])
