@@ -24,12 +24,15 @@ def _i32(a):
     return torch.from_numpy(np.ascontiguousarray(a, dtype=np.int32)).to(DEV)
 
 
+# f = 96: the 16-byte path for every type; 36: 16-byte for fp32, per element for bf16 / fp16; 35: per
+# element for every type
+@pytest.mark.parametrize("f", [96, 36, 35])
 @pytest.mark.parametrize("dt", ["f32", "bf16", "fp16"])
-def test_swiglu_matches_oracle(gpu, oracle, dt):
+def test_swiglu_matches_oracle(gpu, oracle, dt, f):
     tdt = {"f32": torch.float32, "bf16": torch.bfloat16, "fp16": torch.float16}[dt]
     code = {"f32": _lib.JC_F32, "bf16": _lib.JC_BF16, "fp16": _lib.JC_F16}[dt]
     r = np.random.default_rng(7)
-    tokens, f = 301, 96
+    tokens = 301
     up = (3 * r.standard_normal((tokens, 2 * f))).astype(np.float32)
     up[0, 0], up[0, f] = 1e5, 1e5  # saturates in fp16
     ut = _t(up, tdt)
