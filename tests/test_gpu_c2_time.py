@@ -71,6 +71,8 @@ LP_CASES = [c for c in CASES if c[3] % 16 == 0 and c[4] % 8 == 0] + [
     (3, 300, 2, 64, 136, "random"),
     (1, 257, 1, 64, 64, "pad"),
     (2, 512, 3, 64, 192, "random"),
+    (3, 133, 2, 64, 128, "pad"),  # 5 query tiles: one 5-wave workgroup per (row, head)
+    (2, 160, 2, 64, 128, "random"),
 ]
 
 

@@ -51,6 +51,7 @@ CASES = [
     (2, 45, 45, 2, 2, 16, 40, 8, 0.5, False),
     (1, 600, 600, 8, 1, 64, 64, 32, 0.0, True),
     (3, 64, 64, 0, 2, 64, 128, 32, 0.0, False),
+    (2, 136, 130, 4, 2, 64, 128, 32, 0.3, True),  # 140 tokens: 5 query tiles
 ]
 
 
