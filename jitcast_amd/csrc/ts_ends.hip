@@ -73,6 +73,29 @@ __device__ __forceinline__ double seq_prefix(double v, bool take, double& carry)
     return mine;
 }
 
+// Two independent running totals of seq_prefix in one pass over the lanes, so the two chains of
+// dependent adds overlap; each keeps its own step order and rounding.
+__device__ __forceinline__ void seq_prefix2(double va, bool ta, double& ca, double& pa, double vb, bool tb,
+                                            double& cb, double& pb) {
+    const uint64_t ma = __ballot(ta), mb = __ballot(tb);
+    const int lane = threadIdx.x % kWave;
+    double acc_a = ca, acc_b = cb;
+    pa = 0.0;
+    pb = 0.0;
+#pragma unroll
+    for (int k = 0; k < kWave; k++) {
+        const double sa = lane_value(va, k), sb = lane_value(vb, k);
+        if ((ma >> k) & 1) acc_a += sa;
+        if ((mb >> k) & 1) acc_b += sb;
+        if (lane == k) {
+            pa = acc_a;
+            pb = acc_b;
+        }
+    }
+    ca = acc_a;
+    cb = acc_b;
+}
+
 __device__ __forceinline__ float ts_asinh(float v) {
     const double a = fabs((double)v);
     const double r = log(a + sqrt(a * a + 1.0));
@@ -153,30 +176,50 @@ __global__ __launch_bounds__(kWave) void ts_prep_kernel(const PrepArgs a) {
         return;
     }
 
-    // Scaler.causalPatchLocScale: running weighted mean and Welford M2 in double
+    // Scaler.causalPatchLocScale: running weighted mean and Welford M2 in double. Chunk c + 1's cumX
+    // chain runs in the same pass as chunk c's M2 chain (it needs only chunk c's total).
     const double ms = (double)a.minimum_scale;
     double cw = 0.0, cx = 0.0, m2 = 0.0, prev = 0.0;
-    for (int base = 0; base < a.w; base += a.chunk) {
+    struct Chunk {
+        float xf;
+        bool ob, act;
+        double xi, wv, cum_w, cum_x;
+    };
+    auto load = [&](int base, Chunk& c) {
         const int i = base + lane;
-        const bool act = lane < a.chunk && i < a.w;
-        const float xf = act ? x[i] : 0.f;
-        const bool ob = act && obs[i] != 0;
-        const double xi = (double)xf, wv = ob ? 1.0 : 0.0;
-        const uint64_t om = __ballot(ob);
-        const double cum_w = cw + (double)__popcll(om & le);  // counts: exact in any order
+        c.act = lane < a.chunk && i < a.w;
+        c.xf = c.act ? x[i] : 0.f;
+        c.ob = c.act && obs[i] != 0;
+        c.xi = (double)c.xf;
+        c.wv = c.ob ? 1.0 : 0.0;
+        const uint64_t om = __ballot(c.ob);
+        c.cum_w = cw + (double)__popcll(om & le);  // counts: exact in any order
         cw += (double)__popcll(om);
-        const double cum_x = seq_prefix(wv * xi, act, cx);
-        const double mean = cum_x / jmax(cum_w, 1.0);
+    };
+    Chunk cur, nxt;
+    load(0, cur);
+    cur.cum_x = seq_prefix(cur.wv * cur.xi, cur.act, cx);
+    for (int base = 0; base < a.w; base += a.chunk) {
+        const bool more = base + a.chunk < a.w;  // uniform across the wave
+        if (more) load(base + a.chunk, nxt);
+        const double mean = cur.cum_x / jmax(cur.cum_w, 1.0);
         const double before = __shfl(mean, lane == 0 ? 0 : lane - 1);
         const double pm = lane == 0 ? prev : before;
-        const double m2_i = seq_prefix((xi - pm) * (xi - mean) * wv, act, m2);
+        const double term = (cur.xi - pm) * (cur.xi - mean) * cur.wv;
+        double m2_i;
+        if (more) {
+            seq_prefix2(nxt.wv * nxt.xi, nxt.act, cx, nxt.cum_x, term, cur.act, m2, m2_i);
+        } else {
+            m2_i = seq_prefix(term, cur.act, m2);
+        }
         prev = __shfl(mean, a.chunk - 1);
         // at a patch's last step: loc = mean, scale = max(sqrt(M2 / max(max(cumW, 1) - 1, 1)), min)
-        const double var = m2_i / jmax(jmax(cum_w, 1.0) - 1.0, 1.0);
+        const double var = m2_i / jmax(jmax(cur.cum_w, 1.0) - 1.0, 1.0);
         const float pl = (float)mean, ps = (float)jmax(sqrt(var), ms);
         const int last = (lane / a.patch) * a.patch + a.patch - 1;
-        const float l = __shfl(pl, last), s = __shfl(ps, last);
-        if (act) store_step(a, row, i, xf, ob, l, s, a.use_asinh != 0);
+        const float l = __shfl(pl, last), sc = __shfl(ps, last);
+        if (cur.act) store_step(a, row, base + lane, cur.xf, cur.ob, l, sc, a.use_asinh != 0);
+        cur = nxt;
     }
 }
 
