@@ -98,7 +98,8 @@ int jc_plan_adopt(jc_plan *plan, void *dptr, size_t bytes);
 int64_t jc_plan_device_bytes(jc_plan *plan);
 /* The shape key given to jc_plan_begin. */
 uint64_t jc_plan_key(jc_plan *plan);
-/* Waits for the plan's stream, frees the adopted buffers and the graph (idempotent on NULL). */
+/* Waits for the plan's last replay (on whichever stream it was launched), frees the adopted buffers
+ * and the graph (idempotent on NULL). */
 int jc_plan_destroy(jc_plan *plan);
 
 /* ---- synthetic inputs (no reference counterpart: the benchmark's seeded generator) ---------------- */

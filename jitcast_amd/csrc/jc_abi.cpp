@@ -32,6 +32,7 @@ struct jc_plan {
     hipGraphExec_t exec;
     uint64_t key;
     std::vector<std::pair<void*, size_t>> owned;  // device buffers adopted by the plan
+    hipEvent_t done = nullptr;                    // recorded behind every replay, on its stream
 };
 
 namespace {
@@ -508,6 +509,13 @@ int jc_plan_end(jc_ctx* ctx, jc_plan** out) {
     plan->graph = graph;
     plan->exec = exec;
     plan->key = ctx->capture_key;
+    e = hipEventCreateWithFlags(&plan->done, hipEventDisableTiming);
+    if (e != hipSuccess) {
+        (void)hipGraphExecDestroy(exec);
+        (void)hipGraphDestroy(graph);
+        delete plan;
+        return hip_fail("jc_plan_end: hipEventCreateWithFlags", e);
+    }
     *out = plan;
     return JC_OK;
 }
@@ -518,7 +526,11 @@ int jc_plan_launch(jc_plan* plan) {
     if (rc) return rc;
     if (plan->ctx->capturing) return fail(JC_ESTATE, "jc_plan_launch: the context is capturing a plan");
     hipError_t e = hipGraphLaunch(plan->exec, plan->ctx->stream);
-    return e == hipSuccess ? JC_OK : hip_fail("jc_plan_launch", e);
+    if (e != hipSuccess) return hip_fail("jc_plan_launch", e);
+    // jc_plan_destroy waits for this event, so a replay on any stream ends before the graph and
+    // its buffers are released, whatever stream the context launches on by then
+    e = hipEventRecord(plan->done, plan->ctx->stream);
+    return e == hipSuccess ? JC_OK : hip_fail("jc_plan_launch: hipEventRecord", e);
 }
 
 int jc_plan_adopt(jc_plan* plan, void* dptr, size_t bytes) {
@@ -545,8 +557,9 @@ int jc_plan_destroy(jc_plan* plan) {
     if (!plan) return JC_OK;
     (void)hipSetDevice(plan->ctx->device);
     int rc = JC_OK;
-    hipError_t e = hipStreamSynchronize(plan->ctx->stream);  // the graph may still be running
+    hipError_t e = hipEventSynchronize(plan->done);  // the last replay, on whichever stream it ran
     if (e != hipSuccess) rc = hip_fail("jc_plan_destroy", e);
+    (void)hipEventDestroy(plan->done);
     (void)hipGraphExecDestroy(plan->exec);
     (void)hipGraphDestroy(plan->graph);
     for (const auto& b : plan->owned) {
@@ -630,10 +643,9 @@ static int layer_lp(jc_ctx* ctx, const char* W, float* x, const jc_c2_layer_weig
                     const float* table, const int32_t* group_start, const int32_t* group_end, void* workspace, int rows,
                     int n, int d, int heads, int dh, int dff, float eps, int dtype);
 
-int jc_c2_layer(jc_ctx* ctx, float* x, const jc_c2_layer_weights* w, const int32_t* live, const float* table,
-                const int32_t* group_start, const int32_t* group_end, void* workspace, int rows, int n, int d, int heads,
-                int dh, int dff, float eps, int dtype) {
-    const char* W = "jc_c2_layer";
+static int c2_layer(jc_ctx* ctx, const char* W, float* x, const jc_c2_layer_weights* w, const int32_t* live,
+                    const float* table, const int32_t* group_start, const int32_t* group_end, void* workspace, int rows,
+                    int n, int d, int heads, int dh, int dff, float eps, int dtype) {
     int rc = use(ctx, W);
     if (rc) return rc;
     if (rows < 0 || n < 0 || d <= 0 || heads <= 0 || dh <= 0 || dff <= 0)
@@ -679,6 +691,13 @@ int jc_c2_layer(jc_ctx* ctx, float* x, const jc_c2_layer_weights* w, const int32
     return launch_linear(ctx, W, big, dff, static_cast<const float*>(w->wo), w->wo_bias, x, d, T, d, dff, JC_GEMM_ACCUMULATE);
 }
 
+int jc_c2_layer(jc_ctx* ctx, float* x, const jc_c2_layer_weights* w, const int32_t* live, const float* table,
+                const int32_t* group_start, const int32_t* group_end, void* workspace, int rows, int n, int d, int heads,
+                int dh, int dff, float eps, int dtype) {
+    return c2_layer(ctx, "jc_c2_layer", x, w, live, table, group_start, group_end, workspace, rows, n, d, heads, dh,
+                    dff, eps, dtype);
+}
+
 // ---- bf16 / fp16 layer ------------------------------------------------------------------------
 
 static int check_lp_dtype(const char* W, int dtype) {
@@ -704,6 +723,7 @@ static int launch_linear_lp(jc_ctx* ctx, const char* W, const void* a, int lda, 
     if (flags & ~(JC_GEMM_BIAS | JC_GEMM_ACCUMULATE | JC_GEMM_SILU | JC_GEMM_RELU))
         return fail(JC_EINVAL, "%s: unknown flags 0x%x", W, flags);
     if ((flags & JC_GEMM_SILU) && (flags & JC_GEMM_RELU)) return fail(JC_EINVAL, "%s: SILU and RELU together", W);
+    if ((flags & JC_GEMM_BIAS) && !bias) return fail(JC_EINVAL, "%s: JC_GEMM_BIAS without a bias", W);
     if (c_dtype != JC_F32 && (flags & JC_GEMM_ACCUMULATE))
         return fail(JC_EINVAL, "%s: JC_GEMM_ACCUMULATE needs an fp32 C", W);
     jc::GemmLpArgs g{a, w, bias, c, m, n, k, lda, ldc, flags};

@@ -92,7 +92,7 @@ class PlanCache(Generic[K, P]):
             plan = build(key)
             try:
                 result = use(plan)
-            except BaseException as first:
+            except Exception as first:
                 _close_quietly(plan, first)
                 if not self._plans:
                     raise
@@ -100,7 +100,7 @@ class PlanCache(Generic[K, P]):
                 plan = build(key)
                 try:
                     result = use(plan)
-                except BaseException as second:
+                except Exception as second:
                     second.__context__ = first
                     _close_quietly(plan, second)
                     raise

@@ -170,19 +170,43 @@ class HipTimestralModel:
         [rows*(enc+h)] table rows from jc_ts_block_layout, group_start / group_end [rows] and role
         [rows] (or None) as int32 device tensors; rows of a series contiguous."""
         c = self.c
-        n, d, f, heads, dh = enc + h, c.d_model, c.mlp_hidden_dim, c.num_heads, c.head_dim
-        ll = enc - h if covariates else enc
-        tokens_n = rows * n
+        n, d = enc + h, c.d_model
         b = self._buffers(rows, enc, h)
         w = self.w
         ctx = chronos2.context(self.dev.index or 0)
         p = chronos2._ptr
-        lowp = self.code != _lib.JC_F32
         _lib.call("jc_ts_residual", ctx.handle, p(tokens), rows * enc, 2 * c.patch_size, p(w["embed_hidden_w"]),
                   p(w.get("embed_hidden_b")), p(w["embed_output_w"]), p(w.get("embed_output_b")),
                   p(w["embed_residual_w"]), p(w.get("embed_residual_b")), 4 * d, d, p(b["scratch"]), p(b["emb"]))
         _lib.call("jc_ts_assemble", ctx.handle, p(b["emb"]), p(w["query"]), p(b["x"]), rows, enc, n, d)
         x = b["x"]
+        self.encoder(x, key_valid, known, pos, group_start, group_end, role, covariates, rows, enc, h)
+        chronos2.rms_norm(x, w["out_norm"], b["y"], c.norm_eps)
+        _lib.call("jc_ts_gather_decoder", ctx.handle, p(b["y"]), p(b["dec"]), rows, enc, n, h, d)
+        _lib.call("jc_ts_residual", ctx.handle, p(b["dec"]), rows * h, d, p(w["head_hidden_w"]), None,
+                  p(w["head_output_w"]), None, p(w["head_residual_w"]), None, 4 * d, c.patch_size * c.num_quantiles,
+                  p(b["scratch"]), p(b["raw"]))
+        return b["raw"]
+
+    def encoder(self, x, key_valid, known, pos, group_start, group_end, role, covariates: bool, rows: int, enc: int,
+                h: int, mlp: bool = True) -> None:
+        """The encoder layers in place on x (torch fp32 [rows*(enc+h), d] on the GPU), in the order of
+        TimestralForward.Plan's per-layer tasks (TimestralForward.java:335-382): each attention
+        sublayer (RMSNorm, q|k|v and gate projections, time or variate attention with the gate fused,
+        output projection accumulated into x), then the SwiGLU MLP unless mlp is False (the attention
+        stack of the benchmark's config 3). Masks and positions as forward_raw takes them."""
+        import torch
+
+        c = self.c
+        n, d, f, heads, dh = enc + h, c.d_model, c.mlp_hidden_dim, c.num_heads, c.head_dim
+        ll = enc - h if covariates else enc
+        tokens_n = rows * n
+        if tuple(x.shape) != (tokens_n, d) or x.dtype != torch.float32 or not x.is_contiguous():
+            raise _lib.JitcastArgumentError(_lib.JC_EINVAL, f"x must be fp32 [{tokens_n}, {d}]")
+        b = self._buffers(rows, enc, h)
+        ctx = chronos2.context(self.dev.index or 0)
+        p = chronos2._ptr
+        lowp = self.code != _lib.JC_F32
 
         def view(buf, width):  # a contiguous [tokens, width] view of a shared buffer
             return buf.view(-1)[: tokens_n * width].view(tokens_n, width)
@@ -219,18 +243,14 @@ class HipTimestralModel:
                     chronos2.to_lp(att, b["att_lp"])
                     att = b["att_lp"]
                 gemm(att, a["wo"], x, chronos2.GEMM_ACCUMULATE)
+            if not mlp:
+                continue
             hn = norm(lw["mlp_norm"])
             up = view(b["big_lp"] if lowp else b["big"], 2 * f)
             act = b["act_lp"] if lowp else b["act"]
             gemm(hn, lw["up"], up)
             _lib.call("jc_swiglu", ctx.handle, p(up), p(act), tokens_n, f, self.code)
             gemm(act, lw["down"], x, chronos2.GEMM_ACCUMULATE)
-        chronos2.rms_norm(x, w["out_norm"], b["y"], c.norm_eps)
-        _lib.call("jc_ts_gather_decoder", ctx.handle, p(b["y"]), p(b["dec"]), rows, enc, n, h, d)
-        _lib.call("jc_ts_residual", ctx.handle, p(b["dec"]), rows * h, d, p(w["head_hidden_w"]), None,
-                  p(w["head_output_w"]), None, p(w["head_residual_w"]), None, 4 * d, c.patch_size * c.num_quantiles,
-                  p(b["scratch"]), p(b["raw"]))
-        return b["raw"]
 
     def predict_block(self, inputs, observed, group, h: int, role=None, known_future=None, known_future_mask=None):
         """TimestralModel.predict_block on one block, as CpuTimestral.predictBlock runs it

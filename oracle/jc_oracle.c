@@ -39,6 +39,12 @@ static int resolve_threads(int threads) {
     if (threads > 0) {
         return threads;
     }
+    /* the process's CPU share when the environment states it (a GPU box's per-GPU share), else
+       every online CPU */
+    const char *env = getenv("OMP_NUM_THREADS");
+    if (env && atoi(env) > 0) {
+        return atoi(env);
+    }
     long c = sysconf(_SC_NPROCESSORS_ONLN);
     return c > 0 ? (int)c : 1;
 }

@@ -249,6 +249,22 @@ def ts_forward_raw(tokens, w: dict, key_valid, known, position, group, role, cov
     for i in range(rows):
         x[i * n: i * n + enc] = emb[i * enc: (i + 1) * enc]
         x[i * n + enc: (i + 1) * n] = _f32(w["query"])
+    x = ts_encoder(x, w, key_valid, known, position, group, role, covariates, rows, enc, ll, h, heads, dh, rope_dim,
+                   eps, theta, threads)
+    y = rms_norm(x, w["out_norm"], eps)
+    dec = np.concatenate([y[i * n + enc: (i + 1) * n] for i in range(rows)])
+    return ts_residual(dec, w, "head", threads)
+
+
+def ts_encoder(x, w: dict, key_valid, known, position, group, role, covariates, rows, enc, ll, h, heads, dh, rope_dim,
+               eps, theta=10000.0, threads=0, mlp=True) -> np.ndarray:
+    """CpuTimestral.predictBlock's layer loop (CpuTimestral.java:150-172) on x [rows*(enc+h), d]:
+    per layer each attention sublayer (rmsNorm, q|k|v, time attention with RoPE at `position` or
+    variate attention, the sigmoid gate, the output projection added), then the SwiGLU MLP unless
+    mlp is False (the attention-only stack). Returns the new x."""
+    n = enc + h
+    d = x.shape[1]
+    x = _f32(x)
     for lw in w["layers"]:
         for a in lw["attentions"]:
             hn = rms_norm(x, a["norm"], eps)
@@ -261,13 +277,13 @@ def ts_forward_raw(tokens, w: dict, key_valid, known, position, group, role, cov
             if a.get("gate") is not None:
                 att = ts_gate(att, linear(hn, a["gate"], None, threads))
             x = add(x, linear(att, a["wo"], None, threads))
+        if not mlp:
+            continue
         hn = rms_norm(x, lw["mlp_norm"], eps)
         f = lw["down"].shape[1]
         act = swiglu(linear(hn, lw["up"], None, threads), f)
         x = add(x, linear(act, lw["down"], None, threads))
-    y = rms_norm(x, w["out_norm"], eps)
-    dec = np.concatenate([y[i * n + enc: (i + 1) * n] for i in range(rows)])
-    return ts_residual(dec, w, "head", threads)
+    return x
 
 
 def ts_block_prep(window, observed, known, patch, minimum_scale, use_asinh):

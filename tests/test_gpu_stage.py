@@ -232,3 +232,6 @@ def test_layer_rejects_bad_arguments(gpu):
         xb = x.to(torch.bfloat16)
         chronos2.linear_lp(xb, torch.zeros(8, 64, dtype=torch.bfloat16, device=DEV),
                            torch.zeros(10, 8, dtype=torch.bfloat16, device=DEV), flags=chronos2.GEMM_ACCUMULATE)
+    with pytest.raises(JitcastArgumentError):  # JC_GEMM_BIAS with no bias: rejected before any launch
+        chronos2.linear_lp(x.to(torch.bfloat16), torch.zeros(8, 64, dtype=torch.bfloat16, device=DEV),
+                           torch.zeros(10, 8, device=DEV), flags=chronos2.GEMM_BIAS)
