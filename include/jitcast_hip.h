@@ -334,6 +334,22 @@ int jc_c2_layer(jc_ctx *ctx, float *x, const jc_c2_layer_weights *w, const int32
                 int heads, int dh, int dff, float eps, int dtype);
 
 /*
+ * jc_c2_layer without a caller workspace: the layer runs in JC_C2_LAYER_STATIC_BYTES of device memory
+ * the library holds on each GPU it runs on (resolved by jc_init, held until the process ends), and
+ * the call allocates nothing (no hipMalloc, hipFree or allocating library routine). No counterpart
+ * in the reference: it is for callers that cannot allocate (code under hipGraph capture, serving
+ * loops, harnesses that forbid hipMalloc). Arguments and results are jc_c2_layer's; a call whose
+ * jc_c2_layer_workspace_bytes exceeds JC_C2_LAYER_STATIC_BYTES returns JC_EINVAL (split the rows
+ * over several calls). Every call on a GPU shares that GPU's scratch and leaves its contents behind
+ * (the layer writes each part before reading it, so nothing needs clearing): calls that overlap on
+ * one GPU, on any streams or contexts, race.
+ */
+#define JC_C2_LAYER_STATIC_BYTES (64u << 20)
+int jc_c2_layer_static(jc_ctx *ctx, float *x, const jc_c2_layer_weights *w, const int32_t *live, const float *table,
+                       const int32_t *group_start, const int32_t *group_end, int rows, int n, int d, int heads, int dh,
+                       int dff, float eps, int dtype);
+
+/*
  * bf16 / fp16 GEMM with fp32 accumulation: C[m, n] (+)= act(A[m, :k] . W[n, :k] + bias[n]), A and W
  * in the storage type `dtype` (JC_BF16 or JC_F16), bias fp32. c_dtype JC_F32: C fp32, any flags
  * (JC_GEMM_ACCUMULATE adds into C). c_dtype = dtype: C in the storage type, saturated to its finite

@@ -76,6 +76,7 @@ SIGNATURES = {
     "jc_rms_norm": (_i, [_vp, _vp, _vp, _vp, _i, _i, _f]),
     "jc_c2_layer_workspace_bytes": (_c.c_int64, [_i, _i, _i, _i, _i, _i]),
     "jc_c2_layer": (_i, [_vp, _vp, _vp, _i32p, _vp, _i32p, _i32p, _vp, _i, _i, _i, _i, _i, _i, _f, _i]),
+    "jc_c2_layer_static": (_i, [_vp, _vp, _vp, _i32p, _vp, _i32p, _i32p, _i, _i, _i, _i, _i, _i, _f, _i]),
     "jc_linear_lp": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i]),
     "jc_rms_norm_lp": (_i, [_vp, _vp, _vp, _vp, _i, _i, _f, _i]),
     "jc_to_lp": (_i, [_vp, _vp, _vp, _c.c_int64, _i]),

@@ -172,6 +172,22 @@ def layer(x, weights: dict, live, table, group_start, group_end, workspace, rows
               _ptr(group_end), _ptr(workspace), rows, n, d, heads, dh, dff, ctypes.c_float(eps), dtype)
 
 
+# JC_C2_LAYER_STATIC_BYTES: the device scratch jc_c2_layer_static runs in
+LAYER_STATIC_BYTES = 64 << 20
+
+
+def layer_static(x, weights: dict, live, table, group_start, group_end, rows: int, n: int, d: int, heads: int,
+                 dh: int, dff: int, eps: float, dtype: int = _lib.JC_F32) -> None:
+    """layer() without a workspace: jc_c2_layer_static runs the layer in the library's own device
+    scratch (LAYER_STATIC_BYTES per GPU) and allocates nothing; a call whose workspace would exceed it
+    raises JitcastArgumentError. Calls that overlap on one GPU race on that scratch."""
+    _f32(x, "x")
+    ctx = context(x.device.index or 0)
+    lw = LayerWeights.of(weights)
+    _lib.call("jc_c2_layer_static", ctx.handle, _ptr(x), ctypes.byref(lw), _ptr(live), _ptr(table),
+              _ptr(group_start), _ptr(group_end), rows, n, d, heads, dh, dff, ctypes.c_float(eps), dtype)
+
+
 def linear_lp(a, w, c, bias=None, flags: int = 0, m: int | None = None, n: int | None = None, k: int | None = None,
               lda: int | None = None, ldc: int | None = None) -> None:
     """c (+)= act(a . w^T + bias): a and w bfloat16 or float16 (the same), c float32 or that type

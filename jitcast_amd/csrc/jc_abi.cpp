@@ -5,11 +5,13 @@
 
 #include <hip/hip_runtime.h>
 
+#include <climits>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <vector>
 
@@ -90,6 +92,37 @@ int host_fail(int code, const char* fmt, ...) {
 }
 }  // namespace jc
 
+// The workspace of jc_c2_layer_static: device memory in the library's own code object, so that
+// entry point allocates nothing. Each GPU holds its own copy, at its own address, until the process
+// ends. In host code `scratch` names a host-side stand-in, never the device memory: kernels and
+// copies take the address hipGetSymbolAddress returns for the current device (scratch_ptr).
+static __device__ __align__(256) unsigned char scratch[JC_C2_LAYER_STATIC_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];  // per device; set once by jc_init with that device current
+
+// Resolves this device's copy of `scratch` once; the device must be current.
+int scratch_setup(int device) {
+    if (device < 0 || device >= kMaxDevices) return JC_OK;  // jc_c2_layer_static then reports it
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[device]) return JC_OK;
+    void* p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail("jc_init: hipGetSymbolAddress(scratch)", e);
+    if (!p) return fail(JC_EHIP, "jc_init: hipGetSymbolAddress(scratch) returned a null address");
+    g_scratch_ptr[device] = p;
+    return JC_OK;
+}
+
+void* scratch_ptr(int device) {
+    if (device < 0 || device >= kMaxDevices) return nullptr;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    return g_scratch_ptr[device];
+}
+}  // namespace
+
 extern "C" {
 
 const char* jc_last_error(void) { return g_err; }
@@ -110,6 +143,8 @@ int jc_init(int device, jc_ctx** out) {
     hipDeviceProp_t prop;
     e = hipGetDeviceProperties(&prop, device);
     if (e != hipSuccess) return hip_fail("jc_init: hipGetDeviceProperties", e);
+    int src = scratch_setup(device);
+    if (src) return src;
     jc_ctx* ctx = new (std::nothrow) jc_ctx();
     if (!ctx) return fail(JC_ENOMEM, "jc_init: out of host memory");
     ctx->device = device;
@@ -696,6 +731,27 @@ int jc_c2_layer(jc_ctx* ctx, float* x, const jc_c2_layer_weights* w, const int32
                 int dh, int dff, float eps, int dtype) {
     return c2_layer(ctx, "jc_c2_layer", x, w, live, table, group_start, group_end, workspace, rows, n, d, heads, dh,
                     dff, eps, dtype);
+}
+
+int jc_c2_layer_static(jc_ctx* ctx, float* x, const jc_c2_layer_weights* w, const int32_t* live, const float* table,
+                       const int32_t* group_start, const int32_t* group_end, int rows, int n, int d, int heads, int dh,
+                       int dff, float eps, int dtype) {
+    const char* W = "jc_c2_layer_static";
+    if (!ctx) return fail(JC_EINVAL, "%s: null context", W);
+    if (rows < 0 || n < 0 || d <= 0 || heads <= 0 || dh <= 0 || dff <= 0)
+        return fail(JC_EINVAL, "%s: sizes must be positive (rows=%d n=%d d=%d heads=%d dh=%d dff=%d)", W, rows, n, d,
+                    heads, dh, dff);
+    if ((int64_t)heads * dh > INT32_MAX / 12) return fail(JC_EINVAL, "%s: heads * dh too large", W);
+    const int64_t need = jc_c2_layer_workspace_bytes(rows, n, d, heads * dh, dff, dtype);
+    if (need < 0) return fail(JC_EINVAL, "%s: dtype must be JC_F32, JC_BF16 or JC_F16 (got %d)", W, dtype);
+    if (need > (int64_t)JC_C2_LAYER_STATIC_BYTES)
+        return fail(JC_EINVAL,
+                    "%s: %d rows x %d tokens need %lld bytes of workspace, past the %lld-byte static scratch "
+                    "(split the rows over several calls, or use jc_c2_layer with a caller workspace)",
+                    W, rows, n, (long long)need, (long long)JC_C2_LAYER_STATIC_BYTES);
+    void* ws = scratch_ptr(ctx->device);
+    if (!ws) return fail(JC_EUNSUPPORTED, "%s: no static scratch on device %d", W, ctx->device);
+    return c2_layer(ctx, W, x, w, live, table, group_start, group_end, ws, rows, n, d, heads, dh, dff, eps, dtype);
 }
 
 // ---- bf16 / fp16 layer ------------------------------------------------------------------------

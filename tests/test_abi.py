@@ -40,3 +40,22 @@ def test_null_context_is_an_error_not_a_crash():
 
 def test_version():
     assert _lib.lib().jc_version() >= 1
+
+
+def test_static_layer_scratch_size_matches_header():
+    """The Python binding's LAYER_STATIC_BYTES is the header's JC_C2_LAYER_STATIC_BYTES."""
+    import re
+
+    from jitcast_amd import chronos2
+
+    text = _lib.HEADER.read_text()
+    m = re.search(r"#define JC_C2_LAYER_STATIC_BYTES \((\d+)u << (\d+)\)", text)
+    assert m, "JC_C2_LAYER_STATIC_BYTES not found"
+    assert chronos2.LAYER_STATIC_BYTES == int(m.group(1)) << int(m.group(2))
+
+
+def test_static_layer_null_context_is_an_error():
+    rc = _lib.lib().jc_c2_layer_static(None, None, None, None, None, None, None, 1, 1, 64, 1, 64, 64,
+                                       ctypes.c_float(1e-6), 0)
+    assert rc == _lib.JC_EINVAL
+    assert "null context" in _lib.last_error()
