@@ -38,7 +38,7 @@ class Chronos2Config:
     d_ff: int = 3072
     num_layers: int = 12
     num_heads: int = 12
-    layer_norm_eps: float = 1e-6
+    layer_norm_eps: float = float(np.float32(1e-6))  # Chronos2Config keeps it as a float
     rope_theta: float = 10000.0
     context_length: int = 8192
     patch_size: int = 16
@@ -59,6 +59,31 @@ class Chronos2Config:
     @property
     def vocab_size(self) -> int:
         return 2 if self.use_reg_token else 1
+
+    def quantile_levels(self) -> np.ndarray:
+        """The levels as forecasts report them: each double rounded to float (Chronos2Config.quantileLevels)."""
+        return np.asarray(self.quantiles, np.float64).astype(np.float32)
+
+    def prediction_length(self) -> int:
+        """The steps one forward pass forecasts before the long-horizon unrolling."""
+        return self.max_output_patches * self.patch_size
+
+    @staticmethod
+    def from_json(text: str) -> "Chronos2Config":
+        """Chronos2Config.fromJson (J/chronos2/Chronos2Config.java:118-166): a config.json document with
+        only the known keys (unknown ones fail), a Chronos2Model with the ReLU feed-forward layer,
+        float32 weights, equal input/output patch sizes and stride; the missing values take the
+        reference's defaults. ValueError on anything else."""
+        from .checkpoint import parse_config
+
+        return parse_config(text)
+
+    @staticmethod
+    def load(path) -> "Chronos2Config":
+        """Chronos2Config.load: from_json of the file at path."""
+        from pathlib import Path
+
+        return Chronos2Config.from_json(Path(path).read_text(encoding="utf-8"))
 
 
 def random_weights(c: Chronos2Config, seed: int = 0, std: float = 0.02) -> dict:
@@ -256,10 +281,12 @@ class HipChronos2Model:
             self._bufs[key] = self._alloc(rows, nc, h)
         return self._bufs[key]
 
-    def forward_raw(self, tokens, live, group_start, group_end, rows: int, nc: int, h: int, bufs: dict | None = None):
+    def forward_raw(self, tokens, live, group_start, group_end, rows: int, nc: int, h: int, bufs: dict | None = None,
+                    sink=None):
         """The device forward from prepared tokens (torch [rows*(nc+h), 3P] on the GPU) to the raw
         output patch embedding [rows*h, Q*P] on the GPU; rows grouped contiguously. bufs: a plan's
-        buffers (default: the eager forward's)."""
+        buffers (default: the eager forward's). sink(name, x), when given, sees the encoder's x after
+        each layer ("layer0", ...), as the reference's StageSink (CpuChronos2.java:160)."""
         c = self.c
         nreg = 1 if c.use_reg_token else 0
         n, ne, d, ff = nc + nreg + h, nc + h, c.d_model, c.d_ff
@@ -271,9 +298,11 @@ class HipChronos2Model:
                   p(w["in_hidden_b"]), p(w["in_output_w"]), p(w["in_output_b"]), p(w["in_residual_w"]),
                   p(w["in_residual_b"]), ff, d, p(b["scratch"]), p(b["emb"]))
         _lib.call("jc_c2_assemble", ctx.handle, p(b["emb"]), p(self.reg), p(b["x"]), rows, nc, nreg, n, d)
-        for lw in self.layers:
+        for li, lw in enumerate(self.layers):
             chronos2.layer(b["x"], lw, live, b["table"], group_start, group_end, b["ws"], rows, n, d, c.num_heads,
                            c.d_kv, ff, c.layer_norm_eps, self.code)
+            if sink is not None:
+                sink(f"layer{li}", b["x"])
         chronos2.rms_norm(b["x"], w["final_norm"], b["y"], c.layer_norm_eps)
         _lib.call("jc_c2_gather_future", ctx.handle, p(b["y"]), p(b["dec"]), rows, nc + nreg, n, h, d)
         _lib.call("jc_c2_residual", ctx.handle, p(b["dec"]), rows * h, d, p(w["out_hidden_w"]), p(w["out_hidden_b"]),

@@ -239,3 +239,42 @@ def c2_forecast_config4(groups: int = 1024, per_group: int = 4, t: int = 2048, h
         targets[cov] = False
     group = (np.arange(rows) // (per_group + 1)).astype(np.int32)
     return ctx, group, fut, targets
+
+
+def c2_portable_weights(c, seed: int = 0, std: float = 0.02) -> dict:
+    """Chronos-2 random-init weights from the portable RNG, so every language of a build draws the
+    same values: `shared` and every linear weight N(0, std) (tensor k of the binding order on stream
+    seed * 1000003 + 100 + k), RMSNorm weights 1, biases 0 (config 0's recorded choice). The layout is
+    HipChronos2Model's (q|k|v fused per attention sublayer)."""
+    from .checkpoint import _chronos2_names
+
+    w: dict = {"layers": [dict() for _ in range(c.num_layers)]}
+    for k, (name, shape, key) in enumerate(_chronos2_names(c)):
+        if name.endswith(".bias"):
+            arr = np.zeros(shape, np.float32)
+        elif "layer_norm" in name:
+            arr = np.ones(shape, np.float32)
+        else:
+            count = int(np.prod(shape))
+            arr = rng.normal(rng.stream_seed(seed, 100 + k), count, std).reshape(shape)
+        if isinstance(key, tuple):
+            w["layers"][key[0]][key[1]] = arr
+        else:
+            w[key] = arr
+    for lw in w["layers"]:
+        for kind in ("time", "group"):
+            lw[f"{kind}_qkv"] = np.concatenate([lw.pop(f"{kind}_q"), lw.pop(f"{kind}_k"), lw.pop(f"{kind}_v")])
+    return w
+
+
+def c2_config0_series(rows: int = 4, t: int = 512, seed: int = 0) -> np.ndarray:
+    """Config 0's inputs from the portable RNG: per series A1 sin(2 pi t / 24) + A2 sin(2 pi t / 168) +
+    s t + eps with A1, A2 ~ U(0.5, 2), s ~ U(-0.01, 0.01), eps ~ N(0, 0.1), in double, rounded to
+    float. Returns float32 [rows, t]."""
+    amp = rng.uniform_range(rng.stream_seed(seed, 40), 2 * rows, 0.5, 2.0).reshape(rows, 2)
+    slope = rng.uniform_range(rng.stream_seed(seed, 41), rows, -0.01, 0.01)
+    noise = rng.normal(rng.stream_seed(seed, 42), rows * t, 0.1).reshape(rows, t).astype(np.float64)
+    steps = np.arange(t, dtype=np.float64)
+    x = (amp[:, :1] * np.sin(2 * np.pi * steps / 24) + amp[:, 1:] * np.sin(2 * np.pi * steps / 168)
+         + slope[:, None] * steps + noise)
+    return x.astype(np.float32)

@@ -193,7 +193,7 @@ def c2_residual(x, w: dict, prefix: str, threads=0) -> np.ndarray:
 
 
 def c2_forward_raw(tokens, w: dict, live, group, rows, nc, nreg, h, heads, dh, eps, theta=10000.0,
-                   threads=0) -> np.ndarray:
+                   threads=0, sink=None) -> np.ndarray:
     """CpuChronos2.forward from the patch tokens to the raw output patch embedding
     (CpuChronos2.java:122-169): the input embedding, the context / [REG] / future token order, the
     encoder layers, the final RMSNorm, the future tokens, the output embedding. tokens
@@ -207,11 +207,50 @@ def c2_forward_raw(tokens, w: dict, live, group, rows, nc, nreg, h, heads, dh, e
         if nreg:
             x[i * n + nc] = w["shared"][1]
         x[i * n + nc + nreg: (i + 1) * n] = emb[i * ne + nc: (i + 1) * ne]
-    for lw in w["layers"]:
+    for li, lw in enumerate(w["layers"]):
         x = c2_layer(x, lw, live, group, rows, n, heads, dh, eps, theta, threads)
+        if sink is not None:
+            sink(f"layer{li}", x)
     y = rms_norm(x, w["final_norm"], eps)
     dec = np.concatenate([y[i * n + nc + nreg: (i + 1) * n] for i in range(rows)])
     return c2_residual(dec, w, "out", threads)
+
+
+def c2_model_forward(c, w: dict, context, group, future, output_patches, threads=0, sink=None) -> np.ndarray:
+    """CpuChronos2.forward(ModelInput) (CpuChronos2.java:122-173) end to end on the oracle's pieces:
+    ModelLayout.of's window (the last context_length steps, NaN-padded on the left to whole patches),
+    future covariates and live mask (ModelLayout.java:70-116), ModelPrep.of, the forward and
+    ModelPrep.finish. context [rows][T] (equal lengths), group [rows] (any ids, rows of a group need
+    not be adjacent), future [rows][<= output_patches*P] or None. `c` carries the config fields
+    (patch_size, context_length, use_reg_token, num_heads, d_kv, layer_norm_eps, rope_theta,
+    time_encoding_scale, use_arcsinh, quantiles). sink(name, x) sees each layer's output, as the
+    reference's StageSink. Returns [rows][Q][output_patches*P]."""
+    ps, h = c.patch_size, int(output_patches)
+    if h < 1:
+        raise ValueError(f"output patches must be >= 1, got {h}")
+    ctx = np.asarray(context, np.float32)
+    rows, t = ctx.shape
+    group = _i32(group)
+    if group.shape != (rows,):
+        raise ValueError("group ids must have one entry per row")
+    kept = min(t, c.context_length)
+    padded = (kept + ps - 1) // ps * ps
+    nc = padded // ps
+    window = np.full((rows, padded), np.nan, np.float32)
+    window[:, padded - kept:] = ctx[:, t - kept:]
+    fut = np.full((rows, h * ps), np.nan, np.float32)
+    if future is not None:
+        for i in range(rows):
+            f = np.asarray(future[i], np.float32)
+            if f.size > h * ps:
+                raise ValueError(f"{h} output patches cannot hold {f.size} future steps")
+            fut[i, : f.size] = f
+    nreg = 1 if c.use_reg_token else 0
+    live = c2_live(window, rows, nc, ps, nreg, h)
+    tok, loc, scale = c2_prep(window, fut, nc, h, ps, c.time_encoding_scale, c.use_arcsinh)
+    raw = c2_forward_raw(tok, w, live, group, rows, nc, nreg, h, c.num_heads, c.d_kv, c.layer_norm_eps, c.rope_theta,
+                         threads, sink=sink)
+    return c2_finish(raw, loc, scale, rows, h, len(c.quantiles), ps, c.use_arcsinh)
 
 
 def silu(x) -> np.ndarray:
