@@ -31,7 +31,9 @@ from dataclasses import dataclass
 
 import numpy as np
 
-from . import _lib, chronos2, timestral
+from . import _lib, chronos2, chronos2_model, timestral
+from . import options as opts
+from . import plans as plans_mod
 
 QUANTILES_9 = (0.1, 0.2, 0.3, 0.4, 0.5, 0.6, 0.7, 0.8, 0.9)
 
@@ -115,7 +117,13 @@ class HipTimestralModel:
     time attention and SwiGLU run in the storage type, the variate attention reads fp32 q|k|v, the
     residual stream, norms' inputs, the embedding and the head stay fp32."""
 
-    def __init__(self, c: TimestralConfig, weights: dict, dtype: str = "f32", device: int = 0):
+    def __init__(self, c: TimestralConfig, weights: dict, dtype: str = "f32", device: int = 0, max_plans: int = 0,
+                 plan_bytes: int | None = None, buckets: bool | None = None):
+        """max_plans > 0 runs predict_block's device forward from captured plans, one hipGraph per
+        Shape(rows, encoder, horizon, covariates) (TimestralForward.Shape, TimestralForward.java:135),
+        kept in a PlanCache of at most max_plans within plan_bytes of plan buffers (default: no limit);
+        the weights are uploaded once and shared by every plan. buckets (default -Dtimestral.hip.buckets,
+        true) pads each block to a shared shape first (bucketed, TimestralForward.java:81-99, 186-232)."""
         import torch
 
         self.c, self.dtype = c, dtype
@@ -138,40 +146,55 @@ class HipTimestralModel:
                         "mlp_norm": t(lw["mlp_norm"]), "up": lp(lw["up"]), "down": lp(lw["down"])}
                        for lw in weights["layers"]]
         self._bufs = {}
+        self.buckets = opts.boolean("timestral.hip.buckets", True) if buckets is None else bool(buckets)
+        self.plans = None
+        if max_plans > 0:
+            self.plans = plans_mod.PlanCache(max_plans, plan_bytes if plan_bytes else 1 << 62)
+            self._stream = torch.cuda.Stream(self.dev)  # default priority; plans capture and replay on it
 
-    def _buffers(self, rows: int, enc: int, h: int):
+    def _alloc(self, rows: int, enc: int, h: int, inputs: bool = False) -> dict:
+        """One shape's device buffers; with inputs, also the per-call inputs a plan replays from
+        (tokens, key validity, known rows, positions, group bounds, roles)."""
         import torch
 
+        c = self.c
+        n, d, f = enc + h, c.d_model, c.mlp_hidden_dim
+        tokens = rows * n
+        e = lambda *s: torch.empty(*s, dtype=torch.float32, device=self.dev)  # noqa: E731
+        b = {
+            "emb": e(rows * enc, d), "scratch": e(max(rows * enc, rows * h), 4 * d), "x": e(tokens, d),
+            "hn": e(tokens, d), "big": e(tokens, max(3 * d, 2 * f)), "att": e(tokens, d), "gate": e(tokens, d),
+            "act": e(tokens, f), "y": e(tokens, d), "dec": e(rows * h, d),
+            "raw": e(rows * h, c.patch_size * c.num_quantiles),
+            "table": torch.from_numpy(timestral.rope_table(enc, n, c.head_dim, c.rope_dim, c.rope_theta)).to(self.dev),
+        }
+        if self.code != _lib.JC_F32:
+            s = lambda *sh: torch.empty(*sh, dtype=self.tdt, device=self.dev)  # noqa: E731
+            b.update({"hn_lp": s(tokens, d), "big_lp": s(tokens, max(3 * d, 2 * f)), "att_lp": s(tokens, d),
+                      "gate_lp": s(tokens, d), "act_lp": s(tokens, f)})
+        if inputs:
+            i32 = lambda m: torch.zeros(m, dtype=torch.int32, device=self.dev)  # noqa: E731
+            b.update({"tok": e(rows * enc, 2 * c.patch_size), "kv": i32(rows * enc), "known": i32(rows),
+                      "pos": i32(rows * n), "gs": i32(rows), "ge": i32(rows), "role": i32(rows)})
+        return b
+
+    def _buffers(self, rows: int, enc: int, h: int):
         key = (rows, enc, h)
         if key not in self._bufs:
-            self._bufs.clear()
-            c = self.c
-            n, d, f = enc + h, c.d_model, c.mlp_hidden_dim
-            tokens = rows * n
-            e = lambda *s: torch.empty(*s, dtype=torch.float32, device=self.dev)  # noqa: E731
-            b = {
-                "emb": e(rows * enc, d), "scratch": e(max(rows * enc, rows * h), 4 * d), "x": e(tokens, d),
-                "hn": e(tokens, d), "big": e(tokens, max(3 * d, 2 * f)), "att": e(tokens, d), "gate": e(tokens, d),
-                "act": e(tokens, f), "y": e(tokens, d), "dec": e(rows * h, d),
-                "raw": e(rows * h, c.patch_size * c.num_quantiles),
-                "table": torch.from_numpy(timestral.rope_table(enc, n, c.head_dim, c.rope_dim, c.rope_theta)).to(self.dev),
-            }
-            if self.code != _lib.JC_F32:
-                s = lambda *sh: torch.empty(*sh, dtype=self.tdt, device=self.dev)  # noqa: E731
-                b.update({"hn_lp": s(tokens, d), "big_lp": s(tokens, max(3 * d, 2 * f)), "att_lp": s(tokens, d),
-                          "gate_lp": s(tokens, d), "act_lp": s(tokens, f)})
-            self._bufs[key] = b
+            self._bufs.clear()  # the eager forward keeps one shape's buffers
+            self._bufs[key] = self._alloc(rows, enc, h)
         return self._bufs[key]
 
     def forward_raw(self, tokens, key_valid, known, pos, group_start, group_end, role, covariates: bool, rows: int,
-                    enc: int, h: int):
+                    enc: int, h: int, bufs: dict | None = None):
         """The device forward from the patch tokens (torch [rows*enc, 2P] on the GPU) to the head's
         raw outputs [rows*h, P*Q] on the GPU. key_valid [rows*enc], known [rows] (or None), pos
         [rows*(enc+h)] table rows from jc_ts_block_layout, group_start / group_end [rows] and role
-        [rows] (or None) as int32 device tensors; rows of a series contiguous."""
+        [rows] (or None) as int32 device tensors; rows of a series contiguous. bufs: a plan's buffers
+        (default: the eager forward's)."""
         c = self.c
         n, d = enc + h, c.d_model
-        b = self._buffers(rows, enc, h)
+        b = bufs if bufs is not None else self._buffers(rows, enc, h)
         w = self.w
         ctx = chronos2.context(self.dev.index or 0)
         p = chronos2._ptr
@@ -180,7 +203,7 @@ class HipTimestralModel:
                   p(w["embed_residual_w"]), p(w.get("embed_residual_b")), 4 * d, d, p(b["scratch"]), p(b["emb"]))
         _lib.call("jc_ts_assemble", ctx.handle, p(b["emb"]), p(w["query"]), p(b["x"]), rows, enc, n, d)
         x = b["x"]
-        self.encoder(x, key_valid, known, pos, group_start, group_end, role, covariates, rows, enc, h)
+        self.encoder(x, key_valid, known, pos, group_start, group_end, role, covariates, rows, enc, h, bufs=b)
         chronos2.rms_norm(x, w["out_norm"], b["y"], c.norm_eps)
         _lib.call("jc_ts_gather_decoder", ctx.handle, p(b["y"]), p(b["dec"]), rows, enc, n, h, d)
         _lib.call("jc_ts_residual", ctx.handle, p(b["dec"]), rows * h, d, p(w["head_hidden_w"]), None,
@@ -189,7 +212,7 @@ class HipTimestralModel:
         return b["raw"]
 
     def encoder(self, x, key_valid, known, pos, group_start, group_end, role, covariates: bool, rows: int, enc: int,
-                h: int, mlp: bool = True) -> None:
+                h: int, mlp: bool = True, bufs: dict | None = None) -> None:
         """The encoder layers in place on x (torch fp32 [rows*(enc+h), d] on the GPU), in the order of
         TimestralForward.Plan's per-layer tasks (TimestralForward.java:335-382): each attention
         sublayer (RMSNorm, q|k|v and gate projections, time or variate attention with the gate fused,
@@ -203,7 +226,7 @@ class HipTimestralModel:
         tokens_n = rows * n
         if tuple(x.shape) != (tokens_n, d) or x.dtype != torch.float32 or not x.is_contiguous():
             raise _lib.JitcastArgumentError(_lib.JC_EINVAL, f"x must be fp32 [{tokens_n}, {d}]")
-        b = self._buffers(rows, enc, h)
+        b = bufs if bufs is not None else self._buffers(rows, enc, h)
         ctx = chronos2.context(self.dev.index or 0)
         p = chronos2._ptr
         lowp = self.code != _lib.JC_F32
@@ -253,6 +276,18 @@ class HipTimestralModel:
             gemm(act, lw["down"], x, chronos2.GEMM_ACCUMULATE)
 
     def predict_block(self, inputs, observed, group, h: int, role=None, known_future=None, known_future_mask=None):
+        """TimestralForward.predictBlock (TimestralForward.java:186-195): with buckets on, the block padded
+        to its shared shape (leading empty patches, empty series of their own; neither is ever a valid
+        key and positions count from each series' first observation, so the real rows' forecasts do
+        not change), and the real rows' forecasts returned. See predict_exact."""
+        if self.buckets:
+            padded = bucketed(inputs, observed, group, h, role, known_future, known_future_mask, self.c.patch_size)
+            if padded is not None:
+                rows = np.asarray(inputs).shape[0]
+                return self.predict_exact(*padded)[:rows]
+        return self.predict_exact(inputs, observed, group, h, role, known_future, known_future_mask)
+
+    def predict_exact(self, inputs, observed, group, h: int, role=None, known_future=None, known_future_mask=None):
         """TimestralModel.predict_block on one block, as CpuTimestral.predictBlock runs it
         (J/timestral/cpu/CpuTimestral.java:127-188): BlockLayout's window and masks on the host
         (block_window, jc_ts_block_layout), then on the device BlockPrep (jc_ts_prep), the forward and
@@ -286,13 +321,104 @@ class HipTimestralModel:
         scale = torch.empty(rows, wlen, dtype=torch.float32, device=dev)
         _lib.call("jc_ts_prep", ctx.handle, p(win_d), p(obs_d), rows, wlen, ps, p(known_d), c.minimum_scale,
                   int(c.use_asinh), p(tok), None, p(loc), p(scale))
-        raw = self.forward_raw(tok, up(kv.reshape(-1)), known_d, up(pos.reshape(-1)), up(gs), up(ge),
-                               up(role) if cov else None, cov, rows, enc, h)
+        kv_d, pos_d, gs_d, ge_d = up(kv.reshape(-1)), up(pos.reshape(-1)), up(gs), up(ge)
+        role_d = up(role) if cov else None
+        if self.plans is not None:
+            raw = self._forward_planned(tok, kv_d, known_d, pos_d, gs_d, ge_d, role_d, cov, rows, enc, h)
+        else:
+            raw = self.forward_raw(tok, kv_d, known_d, pos_d, gs_d, ge_d, role_d, cov, rows, enc, h)
         out = torch.empty(rows, h * ps, q, dtype=torch.float32, device=dev)
         widths = quantile_widths(c)
         _lib.call("jc_ts_finish", ctx.handle, p(raw), p(loc), p(scale), rows, wlen, t // ps, h, ps, q,
                   widths.ctypes.data, c.median_index, int(c.use_asinh), p(out))
         return out.cpu().numpy()
+
+
+    def _forward_planned(self, tok, kv, known, pos, gs, ge, role, cov: bool, rows: int, enc: int, h: int):
+        """The forward replayed from the plan of Shape(rows, encoder, horizon, covariates)
+        (TimestralForward.predictExact's plans.run): the per-call inputs copied into the plan's buffers,
+        then its captured forward on the model's stream; returns the plan's raw output."""
+        import torch
+
+        shape = (rows, enc, h, bool(cov))
+        cur = torch.cuda.current_stream(self.dev)
+        self._stream.wait_stream(cur)
+
+        def use(plan):
+            b = plan.bufs
+            with torch.cuda.stream(self._stream):
+                b["tok"].copy_(tok)
+                b["kv"].copy_(kv)
+                b["known"].copy_(known)
+                b["pos"].copy_(pos)
+                b["gs"].copy_(gs)
+                b["ge"].copy_(ge)
+                if role is not None:
+                    b["role"].copy_(role)
+                plan.graph.launch()
+            cur.wait_stream(self._stream)
+            return b["raw"]
+
+        return self.plans.run(shape, self._capture, use)
+
+    def _capture(self, shape) -> "chronos2_model.ShapePlan":
+        """TimestralForward.Plan's constructor: the shape's buffers, then the device forward captured
+        into one hipGraph on the model's stream."""
+        import torch
+
+        rows, enc, h, cov = shape
+        b = self._alloc(rows, enc, h, inputs=True)
+        key = (rows << 40) | (enc << 20) | (h << 1) | int(cov)
+        with torch.cuda.stream(self._stream):
+            with plans_mod.capture(key, self.dev.index or 0) as box:
+                self.forward_raw(b["tok"], b["kv"], b["known"], b["pos"], b["gs"], b["ge"], b["role"] if cov else None,
+                                 cov, rows, enc, h, bufs=b)
+        return chronos2_model.ShapePlan(box[0], b)
+
+    def close(self) -> None:
+        """Closes every cached plan (TimestralForward.close)."""
+        if self.plans is not None:
+            self.plans.close()
+
+
+def bucket(x: int) -> int:
+    """TimestralForward.bucket (TimestralForward.java:81-99): x itself up to 8, then the next multiple
+    of a quarter of its power of two (9-16 in steps of 2, 17-32 in steps of 4, ...), so padding adds
+    at most 25% and the number of shapes grows with the logarithm of the size."""
+    if x <= 8:
+        return x
+    step = (1 << ((x - 1).bit_length() - 1)) // 4
+    return (x + step - 1) // step * step
+
+
+def bucketed(inputs, observed, group, h: int, role, known_future, known_future_mask, patch: int):
+    """TimestralForward.bucketed (TimestralForward.java:197-232): the block padded to bucket(patches)
+    patches (leading steps unobserved zeros) and bucket(rows) rows (each added row an empty target
+    series of its own), as (inputs, observed, group, h, role, known_future, known_future_mask); None
+    when the block already has a shared shape."""
+    x = np.asarray(inputs, np.float32)
+    r, t = x.shape
+    patches = t // patch
+    pad_patches, rows = bucket(patches), bucket(r)
+    if pad_patches == patches and rows == r:
+        return None
+    lead, length = (pad_patches - patches) * patch, pad_patches * patch
+    xi = np.zeros((rows, length), np.float32)
+    ob = np.zeros((rows, length), bool)
+    xi[:r, lead:lead + t] = x
+    ob[:r, lead:lead + t] = np.asarray(observed, bool)
+    g = np.asarray(group, np.int32)
+    next_group = (int(g.max()) if g.size else 0) + 1
+    grp = np.concatenate([g, np.arange(next_group, next_group + rows - r, dtype=np.int32)])
+    rl = None if role is None else np.concatenate([np.asarray(role, np.int32), np.zeros(rows - r, np.int32)])
+    kf = kfm = None
+    if known_future is not None:
+        f = np.asarray(known_future, np.float32)
+        kf = np.zeros((rows, f.shape[1]), np.float32)
+        kf[:r] = f
+        kfm = np.zeros((rows, f.shape[1]), bool)
+        kfm[:r] = np.asarray(known_future_mask, bool)
+    return xi, ob, grp, h, rl, kf, kfm
 
 
 FLOAT32_EPS = np.float32(np.finfo(np.float32).eps)

@@ -534,3 +534,68 @@ def rel_max_error(actual, expected) -> float:
     d = np.abs(np.where(an, 0, a) - np.where(en, 0, e))
     scale = max(float(np.max(np.abs(np.where(en, 0, e)))), 1e-6)
     return float(np.max(d)) / scale
+
+
+def ts_block_layout(inputs, observed, group, h, patch, role=None, known_future=None, known_future_mask=None,
+                    covariate_enabled=True, attend_missing=True, block_size=64):
+    """BlockLayout.of (J/timestral/BlockLayout.java:77-148) and position() (203-207), row by row:
+    the window (the context, plus the horizon's known-future steps when some row is a covariate),
+    keyValid per encoder patch (observed, or with attend_missing any patch from the row's first
+    observed one on), the first patch any row of the series observes (0 if none), known rows. Returns
+    (window [rows, enc*P], window_observed, enc, covariates, key_valid [rows, enc] int32, known [rows]
+    int32, position [rows, enc+h] int32, ll). ValueError as BlockLayout.of's IllegalArgumentExceptions."""
+    x = np.asarray(inputs, np.float32)
+    obs_in = np.asarray(observed, bool)
+    rows, t = x.shape
+    if t % patch:
+        raise ValueError(f"context length {t} is not a multiple of the patch size {patch}")
+    if h < 1:
+        raise ValueError(f"horizon patches must be >= 1, got {h}")
+    cov = False
+    if role is not None and covariate_enabled:
+        for v in role:
+            cov = cov or int(v) != 0
+    ll = t // patch
+    window, wobs = x, obs_in
+    roles = [0] * rows
+    if cov:
+        if h > block_size:
+            raise ValueError(f"a block with covariates decodes at most {block_size} patches, got {h}")
+        roles = [int(v) for v in role]
+        window = np.zeros((rows, t + h * patch), np.float32)
+        wobs = np.zeros((rows, t + h * patch), bool)
+        for i in range(rows):
+            window[i, :t] = x[i]
+            wobs[i, :t] = obs_in[i]
+            if known_future is not None:
+                window[i, t:] = np.asarray(known_future[i], np.float32)[: h * patch]
+                wobs[i, t:] = np.asarray(known_future_mask[i], bool)[: h * patch]
+    enc = window.shape[1] // patch
+    valid = np.zeros((rows, enc), np.int32)
+    patch_obs = np.zeros((rows, enc), bool)
+    for i in range(rows):
+        started = False
+        for p in range(enc):
+            anyo = False
+            for s in range(p * patch, (p + 1) * patch):
+                anyo = anyo or bool(wobs[i][s])
+            patch_obs[i][p] = anyo
+            started = started or anyo
+            valid[i][p] = 1 if (started if attend_missing else anyo) else 0
+    group_first = {}
+    for i in range(rows):
+        f = enc
+        for p in range(enc):
+            if patch_obs[i][p]:
+                f = p
+                break
+        g = int(group[i])
+        group_first[g] = min(group_first.get(g, f), f)
+    position = np.zeros((rows, enc + h), np.int32)
+    for i in range(rows):
+        f = group_first[int(group[i])]
+        first = 0 if f == enc else f
+        for k in range(enc + h):
+            position[i][k] = (k if k < enc else ll + k - enc) - first
+    known = np.array([1 if cov and roles[i] == 2 else 0 for i in range(rows)], np.int32)
+    return window, wobs, enc, cov, valid, known, position, ll

@@ -194,3 +194,24 @@ def test_ends_reject_bad_arguments(gpu):
         _lib.call("jc_ts_finish", ctx.handle, p, p, p, 1, 16, 1, 1, 16, 40, w.ctypes.data, 20, 1, p)
     with pytest.raises(_lib.JitcastError, match="exceeds the window"):
         _lib.call("jc_ts_finish", ctx.handle, p, p, p, 1, 16, 2, 1, 16, 3, w.ctypes.data, 1, 1, p)
+
+
+@pytest.mark.parametrize("extra", [0, 2])
+def test_finish_anchor_closed_form(gpu, extra):
+    """jc_ts_finish's frame is the window's step (ll - 1) * P (BlockPrep.java:91-95): with loc and
+    scale different at every step and one (median) level, each output is sinh(m) * scale[a] + loc[a]
+    (tests/test_oracle_ts_forward.py pins the same closed form on the oracle)."""
+    from tests.test_oracle_ts_forward import _anchor_case, _anchor_expected
+
+    rows, ll, h, ps = 3, 5, 2, 4
+    raw, loc, scale, w = _anchor_case(rows, ll, h, ps, extra)
+    exp = _anchor_expected(raw, loc, scale, rows, ll, h, ps)
+    widths = np.zeros(1, np.float32)
+    p = chronos2._ptr
+    rd, loc_d, scale_d = (torch.from_numpy(a).to(DEV) for a in (raw, loc, scale))
+    out = torch.empty(rows, h * ps, 1, device=DEV)
+    _lib.call("jc_ts_finish", chronos2.context(0).handle, p(rd), p(loc_d), p(scale_d), rows, w, ll, h, ps, 1,
+              widths.ctypes.data, 0, 1, p(out))
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()[:, :, 0]
+    assert _ulps(got, exp) <= 1  # the device's sinh may differ from the host's by one ulp

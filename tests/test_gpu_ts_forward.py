@@ -134,16 +134,16 @@ def test_forward_matches_oracle(gpu, oracle, name, c, rows, groups, enc, h, cova
 
 
 def _oracle_block(oracle, c, x, obs, group, h, role, fut, fut_mask):
-    """CpuTimestral.predictBlock end to end on the oracle's pieces."""
+    """CpuTimestral.predictBlock end to end on the oracle's pieces (its BlockLayout, BlockPrep,
+    forward and finish): nothing of the product's host code."""
     ps = c.patch_size
-    window, wobs, cov = tm.block_window(c, x, obs, role, fut, fut_mask, h)
-    enc, _, kv, known, pos = timestral.block_layout(obs, group, h, ps, role=role if cov else None,
-                                                    future_observed=fut_mask if cov else None)
+    window, wobs, enc, cov, kv, known, position, ll = oracle.ts_block_layout(
+        x, obs, group, h, ps, role, fut, fut_mask, c.covariate_enabled, c.attend_missing, c.block_size)
     tok, _, loc, scale = oracle.ts_block_prep(window, wobs, known, ps, c.minimum_scale, c.use_asinh)
-    rows, t = x.shape
-    ll = t // ps
-    raw = oracle.ts_forward_raw(tok, tm_weights(c), kv, known, pos - enc, group, role if cov else np.zeros(rows, np.int32),
-                                cov, rows, enc, ll, h, c.num_heads, c.head_dim, c.rope_dim, c.norm_eps, c.rope_theta)
+    rows = x.shape[0]
+    raw = oracle.ts_forward_raw(tok, tm_weights(c), kv, known, position, group,
+                                np.asarray(role, np.int32) if cov else np.zeros(rows, np.int32), cov, rows, enc, ll, h,
+                                c.num_heads, c.head_dim, c.rope_dim, c.norm_eps, c.rope_theta)
     return oracle.ts_block_finish(raw, loc, scale, ll, h, ps, c.quantiles, c.median_index, c.quantile_width_factor,
                                   c.use_asinh)
 

@@ -1,5 +1,12 @@
-"""jc_ts_block_layout (the host BlockLayout.of) against an independent pure-Python restatement of
-BlockLayout.java:77-148 and 203-207, on seeded blocks with and without covariates (CPU only)."""
+"""BlockLayout.of on the host.
+
+- The oracle's restatement (oracle.ts_block_layout, BlockLayout.java:77-148, 203-207) is pinned by
+  closed forms: a fully observed block is all valid with positions equal to the token index; a
+  series that starts k patches late is shifted by k; without attend_missing only observed patches
+  are valid; a series no row observes counts from 0; decoder tokens continue from the context
+  patches; known rows exist only on the covariate path; the window holds the known future.
+- jc_ts_block_layout (the product) equals the oracle on seeded blocks with and without covariates.
+"""
 import numpy as np
 import pytest
 
@@ -7,46 +14,11 @@ from jitcast_amd import JitcastArgumentError, rng, timestral
 from tests import cases
 
 
-def _reference_layout(observed, future, group, role, h, patch, cov_enabled, attend_missing):
-    rows, t = observed.shape
-    cov = role is not None and cov_enabled and any(x != 0 for x in role)
-    ll = t // patch
-    if cov:
-        fut = future if future is not None else np.zeros((rows, h * patch), bool)
-        window = np.concatenate([observed.astype(bool), fut.astype(bool)], axis=1)
-    else:
-        window = observed.astype(bool)
-    enc = window.shape[1] // patch
-    valid = np.zeros((rows, enc), bool)
-    first = []
-    for i in range(rows):
-        started = False
-        f = enc
-        for p in range(enc):
-            anyobs = bool(window[i, p * patch:(p + 1) * patch].any())
-            if anyobs and f == enc:
-                f = p
-            started = started or anyobs
-            valid[i, p] = started if attend_missing else anyobs
-        first.append(f)
-    gfirst = {}
-    for i in range(rows):
-        gfirst[group[i]] = min(gfirst.get(group[i], enc), first[i])
-    pos = np.zeros((rows, enc + h), np.int64)
-    for i in range(rows):
-        f = gfirst[group[i]]
-        f = 0 if f == enc else f
-        for k in range(enc + h):
-            pos[i, k] = (k if k < enc else ll + k - enc) - f + enc
-    known = np.array([1 if cov and role[i] == 2 else 0 for i in range(rows)])
-    return enc, cov, valid.astype(np.int32), known, pos
-
-
 @pytest.mark.parametrize("cov_enabled,with_role,with_future,attend", [
     (True, True, True, True), (True, True, False, True), (True, False, False, True), (False, True, True, True),
     (True, True, True, False),
 ])
-def test_block_layout_matches_restatement(cov_enabled, with_role, with_future, attend):
+def test_block_layout_matches_oracle(oracle, cov_enabled, with_role, with_future, attend):
     rows, patch, ll, h = 9, 4, 7, 3
     t = ll * patch
     obs = rng.uniform(rng.stream_seed(5, 7), rows * t).reshape(rows, t) < 0.5
@@ -56,10 +28,14 @@ def test_block_layout_matches_restatement(cov_enabled, with_role, with_future, a
     role = np.floor(rng.uniform(rng.stream_seed(5, 8), rows) * 3).astype(np.int32) if with_role else None
     fut = (rng.uniform(rng.stream_seed(5, 9), rows * h * patch).reshape(rows, h * patch) < 0.7) if with_future else None
     got = timestral.block_layout(obs, group, h, patch, role, fut, cov_enabled, attend)
-    exp = _reference_layout(obs, fut, group, role, h, patch, cov_enabled, attend)
-    assert got[0] == exp[0] and got[1] == exp[1]
-    for a, b in zip(got[2:], exp[2:]):
-        np.testing.assert_array_equal(a, b)
+    x = np.zeros(obs.shape, np.float32)
+    _, _, enc, cov, kv, known, position, _ = oracle.ts_block_layout(
+        x, obs, group, h, patch, role, None if fut is None else np.zeros(fut.shape, np.float32), fut, cov_enabled,
+        attend, block_size=64)
+    assert got[0] == enc and got[1] == cov
+    np.testing.assert_array_equal(got[2], kv)
+    np.testing.assert_array_equal(got[3], known)
+    np.testing.assert_array_equal(got[4], position + enc)  # the product returns table rows
 
 
 def test_block_layout_errors_mirror_block_layout_of():
@@ -70,3 +46,83 @@ def test_block_layout_errors_mirror_block_layout_of():
         timestral.block_layout(np.ones((2, 8), bool), [0, 0], 0, 4)
     with pytest.raises(JitcastArgumentError, match="decodes at most"):
         timestral.block_layout(np.ones((2, 8), bool), [0, 0], 5, 4, role=[0, 2], block_size=4)
+
+
+def test_oracle_layout_closed_forms(oracle):
+    rows, patch, ll, h = 3, 4, 6, 2
+    t = ll * patch
+    x = np.arange(rows * t, dtype=np.float32).reshape(rows, t)
+    full = np.ones((rows, t), bool)
+    win, wobs, enc, cov, kv, known, pos, l2 = oracle.ts_block_layout(x, full, [0, 1, 2], h, patch)
+    assert (enc, cov, l2) == (ll, False, ll)
+    np.testing.assert_array_equal(win, x)
+    assert kv.all() and not known.any()
+    np.testing.assert_array_equal(pos, np.tile(np.arange(enc + h), (rows, 1)))  # decoders continue from ll
+    late = full.copy()
+    late[:, : 2 * patch] = False  # every row of every series starts 2 patches late
+    late[1, 2 * patch] = False  # row 1's third patch still has 3 observed steps
+    _, _, _, _, kv, _, pos, _ = oracle.ts_block_layout(x, late, [0, 1, 2], h, patch)
+    np.testing.assert_array_equal(kv[:, :2], 0)
+    assert kv[:, 2:].all()
+    np.testing.assert_array_equal(pos, np.tile(np.arange(enc + h) - 2, (rows, 1)))
+    gap = full.copy()
+    gap[0, patch: 2 * patch] = False  # an unobserved patch inside the context
+    _, _, _, _, kv_a, _, _, _ = oracle.ts_block_layout(x, gap, [0, 1, 2], h, patch, attend_missing=True)
+    _, _, _, _, kv_o, _, _, _ = oracle.ts_block_layout(x, gap, [0, 1, 2], h, patch, attend_missing=False)
+    assert kv_a[0, 1] == 1 and kv_o[0, 1] == 0
+    none = np.zeros((rows, t), bool)
+    none[2] = True
+    # rows 0 and 1 form a series no row observes: positions from 0; row 2 alone starts at 0 too
+    _, _, _, _, kv, _, pos, _ = oracle.ts_block_layout(x, none, [0, 0, 2], h, patch)
+    assert not kv[:2].any()
+    np.testing.assert_array_equal(pos[0], np.arange(enc + h))
+    # the earliest row of a series sets its origin: row 1 observes from patch 3, row 0 from patch 1
+    two = np.zeros((2, t), bool)
+    two[0, patch:] = True
+    two[1, 3 * patch:] = True
+    _, _, _, _, _, _, pos, _ = oracle.ts_block_layout(x[:2], two, [5, 5], h, patch)
+    np.testing.assert_array_equal(pos, np.tile(np.arange(enc + h) - 1, (2, 1)))
+    # the covariate path: the window gains the horizon's known future, known rows are role 2
+    fut = np.full((rows, h * patch), 7.0, np.float32)
+    fmask = np.zeros((rows, h * patch), bool)
+    fmask[2] = True
+    win, wobs, enc, cov, kv, known, pos, _ = oracle.ts_block_layout(x, full, [0, 0, 0], h, patch, role=[0, 1, 2],
+                                                                     known_future=fut, known_future_mask=fmask)
+    assert cov and enc == ll + h and list(known) == [0, 0, 1]
+    assert (win[:, t:] == 7).all() and wobs[2, t:].all() and not wobs[:2, t:].any()
+    assert list(kv[2, ll:]) == [1] * h and list(kv[0, ll:]) == [1] * h  # attend_missing: started earlier
+    _, _, _, cov_off, _, known_off, _, _ = oracle.ts_block_layout(x, full, [0, 0, 0], h, patch, role=[0, 1, 2],
+                                                                 covariate_enabled=False)
+    assert not cov_off and not known_off.any()
+
+
+def test_bucket_sizes():
+    """TimestralForward.bucket: x up to 8, then multiples of a quarter of the power of two below x."""
+    from jitcast_amd.timestral_model import bucket
+
+    assert [bucket(x) for x in range(1, 9)] == list(range(1, 9))
+    assert [bucket(x) for x in (9, 10, 11, 12, 15, 16)] == [10, 10, 12, 12, 16, 16]
+    assert [bucket(x) for x in (17, 19, 21, 32, 33, 41, 1023, 1024, 1025)] == [20, 20, 24, 32, 40, 48, 1024, 1024, 1280]
+    for x in range(1, 5000):  # at most 25% padding, never less than x
+        assert x <= bucket(x) <= max(x, 1.25 * x)
+
+
+def test_bucketed_pads_leading_patches_and_empty_series():
+    from jitcast_amd.timestral_model import bucketed
+
+    r = np.random.default_rng(3)
+    rows, patch, patches, h = 11, 4, 9, 2
+    x = r.standard_normal((rows, patch * patches)).astype(np.float32)
+    obs = r.random((rows, patch * patches)) > 0.2
+    group = np.repeat(np.arange(4), [3, 3, 3, 2]).astype(np.int32)
+    role = np.tile([0, 1, 2], 4)[:rows].astype(np.int32)
+    kf = r.standard_normal((rows, h * patch)).astype(np.float32)
+    kfm = np.ones((rows, h * patch), bool)
+    xi, ob, g, h2, rl, kf2, kfm2 = bucketed(x, obs, group, h, role, kf, kfm, patch)
+    assert xi.shape == (12, 10 * patch) and h2 == h
+    np.testing.assert_array_equal(xi[:rows, patch:], x)  # one leading empty patch
+    assert not ob[:, :patch].any() and not ob[rows:].any() and (xi[:, :patch] == 0).all()
+    assert list(g) == list(group) + [4] and list(rl) == list(role) + [0]
+    np.testing.assert_array_equal(kf2[:rows], kf)
+    assert not kfm2[rows:].any()
+    assert bucketed(x[:8, :32], obs[:8, :32], group[:8], h, None, None, None, patch) is None  # 8 rows, 8 patches

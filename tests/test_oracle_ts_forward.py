@@ -170,3 +170,41 @@ def test_host_finish_matches_oracle(oracle):
     assert np.all(np.isfinite(got))
     assert got[0, 0, 4] == got[0, 0, 2] > 1e37  # +inf clamped to the step's finite maximum
     np.testing.assert_array_max_ulp(got, exp, maxulp=2)
+
+
+def _anchor_case(rows=3, ll=5, h=2, ps=4, extra_patches=0):
+    """raw medians, and loc / scale that differ at every step of the window (so each step names a
+    distinct frame)."""
+    r = np.random.default_rng(8)
+    w = (ll + extra_patches) * ps
+    raw = r.uniform(-2, 2, (rows * h, ps)).astype(np.float32)
+    loc = (100 * np.arange(rows * w).reshape(rows, w) + 3).astype(np.float32)
+    scale = (1 + 0.01 * np.arange(rows * w).reshape(rows, w)).astype(np.float32)
+    return raw, loc, scale, w
+
+
+def _anchor_expected(raw, loc, scale, rows, ll, h, ps):
+    """sinh(m) * scale[(ll-1)*P] + loc[(ll-1)*P] per step, float multiply then add."""
+    a = (ll - 1) * ps
+    m = np.sinh(raw.astype(np.float64)).astype(np.float32).reshape(rows, h * ps)
+    return ((m * scale[:, a:a + 1]).astype(np.float32) + loc[:, a:a + 1]).astype(np.float32)
+
+
+@pytest.mark.parametrize("extra", [0, 2])
+def test_finish_anchor_closed_form(oracle, extra):
+    """BlockPrep.finish denormalizes every forecast step with the frame at step (ll - 1) * P of the
+    window, the first step of the last context patch (BlockPrep.java:91-95). With one (median) level
+    the quantile map leaves the raw value, so each output is sinh(m) * scale[a] + loc[a] at that
+    anchor; loc and scale differ at every step, so any other anchor fails. extra: a covariate
+    window's horizon patches after the context (w = (ll + h) * P), which the anchor must skip."""
+    rows, ll, h, ps = 3, 5, 2, 4
+    raw, loc, scale, _ = _anchor_case(rows, ll, h, ps, extra)
+    exp = _anchor_expected(raw, loc, scale, rows, ll, h, ps)
+    got = oracle.ts_block_finish(raw, loc, scale, ll, h, ps, (0.5,), 0, 2.0, True)
+    np.testing.assert_array_equal(got[:, :, 0], exp)
+    c = tm.TimestralConfig(patch_size=ps, quantiles=(0.5,))
+    np.testing.assert_array_equal(tm.block_finish(c, raw, loc, scale, ll, h)[:, :, 0], exp)
+    # a wrong anchor is visible: the last step of the context, or (inside a covariate window) step ll * P
+    for wrong in (ll * ps - 1, ll * ps)[: 1 + (extra > 0)]:
+        assert not np.array_equal(exp, ((np.sinh(raw.astype(np.float64)).astype(np.float32).reshape(rows, -1)
+                                         * scale[:, wrong:wrong + 1]) + loc[:, wrong:wrong + 1]).astype(np.float32))
