@@ -20,7 +20,7 @@ OUT_DIR = HERE / "_build"
 LIB = HERE / "libjitcast_hip.so"
 ARCH = os.environ.get("JITCAST_HIP_ARCH", "gfx950")
 
-SOURCES = ["jc_abi.cpp", "jc_host.cpp", "time_attention_f32.hip", "time_attention_lp.hip", "time_attention_lpw.hip", "time_attention_lpp.hip", "gate.hip", "group_attention_f32.hip", "stage_f32.hip", "stage_lp.hip", "c2_tokens.hip", "c2_prep.hip", "ts_block.hip", "ts_ends.hip", "rng.hip"]
+SOURCES = ["jc_abi.cpp", "jc_blas.cpp", "jc_host.cpp", "time_attention_f32.hip", "time_attention_lp.hip", "time_attention_lpw.hip", "time_attention_lpp.hip", "gate.hip", "group_attention_f32.hip", "stage_f32.hip", "stage_lp.hip", "c2_tokens.hip", "c2_prep.hip", "ts_block.hip", "ts_ends.hip", "rng.hip"]
 
 COMMON = [
     "-O3",
@@ -64,7 +64,10 @@ def build(verbose: bool = True) -> Path:
     with cf.ThreadPoolExecutor(max_workers=min(8, len(SOURCES))) as ex:
         objs = list(ex.map(_compile, SOURCES))
     tmp = LIB.with_suffix(".so.tmp")
-    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
+    # hipBLASLt runs the plain GEMMs (jc_blas.cpp); the RPATH finds it where ROCm installs it
+    rocm_lib = str(Path(hipcc()).resolve().parent.parent / "lib")
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs), f"-L{rocm_lib}",
+           "-lhipblaslt", f"-Wl,-rpath,{rocm_lib}"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}{r.stderr}")

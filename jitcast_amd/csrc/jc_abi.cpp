@@ -15,6 +15,7 @@
 #include <new>
 #include <vector>
 
+#include "jc_blas.hpp"
 #include "jc_kernels.hpp"
 
 struct jc_ctx {
@@ -26,6 +27,8 @@ struct jc_ctx {
     bool capturing;          // between jc_plan_begin and jc_plan_end
     hipStream_t capture_on;  // the stream being captured
     uint64_t capture_key;
+    jc::Blas* blas;          // hipBLASLt for the plain GEMMs (nullptr: the library's own kernels)
+    bool own_gemm;           // set while a call must not use hipBLASLt (jc_c2_layer_static)
 };
 
 struct jc_plan {
@@ -78,6 +81,14 @@ LpKernel lp_choice(bool ts) {
     if (e && !strcmp(e, "wide")) return kLpWide;
     if (e && !strcmp(e, "persist")) return kLpPersist;
     return ts ? kLpStream : kLpPersist;
+}
+
+// JITCAST_HIP_GEMM=own runs the plain GEMMs on the library's own MFMA kernels (gemm_f32, gemm_lp)
+// instead of hipBLASLt. Read at every call.
+bool use_blas(const jc_ctx* ctx) {
+    if (!ctx->blas || ctx->own_gemm) return false;
+    const char* e = getenv("JITCAST_HIP_GEMM");
+    return !(e && !strcmp(e, "own"));
 }
 
 }  // namespace
@@ -159,6 +170,8 @@ int jc_init(int device, jc_ctx** out) {
     ctx->capturing = false;
     ctx->capture_on = nullptr;
     ctx->capture_key = 0;
+    ctx->blas = jc::blas_create();  // nullptr leaves the GEMMs on the library's own kernels
+    ctx->own_gemm = false;
     *out = ctx;
     return JC_OK;
 }
@@ -172,6 +185,7 @@ int jc_destroy(jc_ctx* ctx) {
         ctx->capturing = false;
     }
     (void)hipStreamSynchronize(ctx->stream);
+    jc::blas_destroy(ctx->blas);
     (void)hipStreamDestroy(ctx->own);
     delete ctx;
     return JC_OK;
@@ -629,6 +643,12 @@ static int launch_linear(jc_ctx* ctx, const char* W, const float* a, int lda, co
     if (bias) flags |= JC_GEMM_BIAS;
     int rc = check_linear(W, a, lda, w, bias, c, ldc, m, n, k, flags);
     if (rc || (size_t)m * n == 0) return rc;
+    if (use_blas(ctx)) {
+        const jc::BlasStatus bs = jc::blas_gemm(ctx->blas, a, lda, w, bias, c, ldc, m, n, k, flags, JC_F32, JC_F32,
+                                                ctx->stream);
+        if (bs == jc::kBlasDone) return JC_OK;
+        if (bs == jc::kBlasError) return fail(JC_EHIP, "%s: hipblasLtMatmul failed", W);
+    }
     jc::GemmArgs g{a, w, bias, c, m, n, k, lda, ldc, flags};
     hipError_t e = jc::gemm_f32_launch(g, ctx->stream);
     return e == hipSuccess ? JC_OK : hip_fail(W, e);
@@ -751,7 +771,12 @@ int jc_c2_layer_static(jc_ctx* ctx, float* x, const jc_c2_layer_weights* w, cons
                     W, rows, n, (long long)need, (long long)JC_C2_LAYER_STATIC_BYTES);
     void* ws = scratch_ptr(ctx->device);
     if (!ws) return fail(JC_EUNSUPPORTED, "%s: no static scratch on device %d", W, ctx->device);
-    return c2_layer(ctx, W, x, w, live, table, group_start, group_end, ws, rows, n, d, heads, dh, dff, eps, dtype);
+    // the library's own GEMM kernels: no library routine that could allocate
+    ctx->own_gemm = true;
+    const int rc = c2_layer(ctx, W, x, w, live, table, group_start, group_end, ws, rows, n, d, heads, dh, dff, eps,
+                            dtype);
+    ctx->own_gemm = false;
+    return rc;
 }
 
 // ---- bf16 / fp16 layer ------------------------------------------------------------------------
@@ -782,6 +807,12 @@ static int launch_linear_lp(jc_ctx* ctx, const char* W, const void* a, int lda, 
     if ((flags & JC_GEMM_BIAS) && !bias) return fail(JC_EINVAL, "%s: JC_GEMM_BIAS without a bias", W);
     if (c_dtype != JC_F32 && (flags & JC_GEMM_ACCUMULATE))
         return fail(JC_EINVAL, "%s: JC_GEMM_ACCUMULATE needs an fp32 C", W);
+    if (use_blas(ctx)) {
+        const jc::BlasStatus bs = jc::blas_gemm(ctx->blas, a, lda, w, bias, c, ldc, m, n, k, flags, dtype, c_dtype,
+                                                ctx->stream);
+        if (bs == jc::kBlasDone) return JC_OK;
+        if (bs == jc::kBlasError) return fail(JC_EHIP, "%s: hipblasLtMatmul failed", W);
+    }
     jc::GemmLpArgs g{a, w, bias, c, m, n, k, lda, ldc, flags};
     hipError_t e = jc::gemm_lp_launch(g, dtype == JC_F16, c_dtype != JC_F32, ctx->cus, ctx->stream);
     return e == hipSuccess ? JC_OK : hip_fail(W, e);

@@ -62,3 +62,14 @@ def _built_library():
     spec.loader.exec_module(b)
     if not b.LIB.exists():
         b.build(verbose=False)
+
+
+@pytest.fixture(params=["blas", "own"])
+def gemm_path(request, monkeypatch):
+    """Which kernels run the plain GEMMs (JITCAST_HIP_GEMM): hipBLASLt (the default) or the library's
+    own MFMA kernels (gemm_f32, gemm_lp), which also take the combinations hipBLASLt declines."""
+    if request.param == "own":
+        monkeypatch.setenv("JITCAST_HIP_GEMM", "own")
+    else:
+        monkeypatch.delenv("JITCAST_HIP_GEMM", raising=False)
+    return request.param

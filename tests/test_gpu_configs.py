@@ -176,7 +176,9 @@ def test_config4_forecast_matches_oracle(gpu, oracle, dt):
 
 def test_config4_full_request_properties(gpu):
     """Config 4's full request (1,024 groups, 5,120 rows) through the fp32 encoder: finite quantiles,
-    and permuting the groups permutes the forecasts bit for bit."""
+    and permuting the groups permutes the forecasts, to fp32 rounding: every kernel computes a row
+    independently of its slot, but hipBLASLt's algorithm for these GEMM shapes may give output tiles
+    different splits of k, so a row's sums can round differently where it sits."""
     print("case config 4 full request fp32: 1024 groups x 5 rows x 2048 steps", flush=True)
     ctx, group, fut, _ = synthetic.c2_forecast_config4()
     model = cm.HipChronos2Model(C4, _c4_weights(), dtype="f32")
@@ -185,4 +187,6 @@ def test_config4_full_request_properties(gpu):
     gperm = np.random.default_rng(3).permutation(1024)
     rows = (gperm[:, None] * 5 + np.arange(5)[None, :]).reshape(-1)
     b = model.forecast(ctx[rows], group[rows], fut[rows], h=4)
-    np.testing.assert_array_equal(a[rows], b)
+    d = float(np.max(np.abs(a[rows].astype(np.float64) - b)) / np.max(np.abs(b)))
+    print(f"  permuted groups: max rel diff {d:.2e}", flush=True)
+    assert d <= 1e-5

@@ -3,7 +3,8 @@ jc_linear (Kernels.gemm's flags), jc_rms_norm (Kernels.rmsNorm) and jc_c2_layer 
 of Chronos2Forward.Plan, Chronos2Forward.java:258-286) against the oracle.
 
 Bar: max relative error (the reference's metric) <= 1e-4 for the fp32 layer; the GEMM and the norm
-alone are held to 1e-5.
+alone are held to 1e-5. The GEMM and layer tests run on both GEMM paths: hipBLASLt (the default) and
+the library's own MFMA kernels.
 """
 import numpy as np
 import pytest
@@ -39,7 +40,7 @@ def _epilogue(y, c0, bias, flags):
 @pytest.mark.parametrize("flags,bias", [(0, False), (0, True), (chronos2.GEMM_RELU, True),
                                         (chronos2.GEMM_ACCUMULATE, False), (chronos2.GEMM_ACCUMULATE, True),
                                         (chronos2.GEMM_SILU, True), (chronos2.GEMM_RELU | chronos2.GEMM_ACCUMULATE, False)])
-def test_linear_matches_oracle(gpu, oracle, m, n, k, flags, bias):
+def test_linear_matches_oracle(gpu, oracle, gemm_path, m, n, k, flags, bias):
     print(f"case m={m} n={n} k={k} flags={flags} bias={bias}", flush=True)
     r = np.random.default_rng(m * 7 + n * 3 + k + flags)
     a = r.standard_normal((m, k)).astype(np.float32)
@@ -53,7 +54,7 @@ def test_linear_matches_oracle(gpu, oracle, m, n, k, flags, bias):
     assert oracle.rel_max_error(c.cpu().numpy(), exp) <= 1e-5
 
 
-def test_linear_strided_operands(gpu, oracle):
+def test_linear_strided_operands(gpu, oracle, gemm_path):
     """lda > k (a column slice of a wider activation) and ldc > n (writing into a wider buffer)."""
     m, n, k, lda, ldc = 70, 48, 32, 40, 64
     r = np.random.default_rng(3)
@@ -109,7 +110,7 @@ def _run_layer(x, w, live, group, rows, n, heads, dh, dff, eps, dtype=None):
     (4, 37, 8, 64, 512, 2048, False),    # config 0's layer shape (d_model 512, 8 x 64)
     (3, 130, 12, 64, 768, 3072, False),  # config 4's layer shape (d_model 768, 12 x 64), 130 tokens
 ])
-def test_layer_matches_oracle(gpu, oracle, rows, n, heads, dh, d, dff, bias):
+def test_layer_matches_oracle(gpu, oracle, gemm_path, rows, n, heads, dh, d, dff, bias):
     print(f"case rows={rows} n={n} heads={heads} dh={dh} d={d} dff={dff} bias={bias}", flush=True)
     w = _layer_weights(21 + d, d, heads * dh, dff, bias)
     x = np.random.default_rng(22).standard_normal((rows * n, d)).astype(np.float32)
@@ -132,7 +133,7 @@ LP = {"bf16": torch.bfloat16, "fp16": torch.float16}
 @pytest.mark.parametrize("flags,bias,out", [(0, False, "lp"), (chronos2.GEMM_RELU, True, "lp"), (0, True, "f32"),
                                             (chronos2.GEMM_ACCUMULATE, False, "f32"),
                                             (chronos2.GEMM_RELU | chronos2.GEMM_ACCUMULATE, True, "f32")])
-def test_linear_lp_matches_oracle(gpu, oracle, m, n, k, flags, bias, out, dt):
+def test_linear_lp_matches_oracle(gpu, oracle, gemm_path, m, n, k, flags, bias, out, dt):
     """bf16/fp16 GEMM: exact to fp32-accumulation rounding of the rounded operands (the oracle on
     the same rounded values), then rounded to the output type."""
     print(f"case {dt} m={m} n={n} k={k} flags={flags} bias={bias} out={out}", flush=True)
@@ -152,7 +153,7 @@ def test_linear_lp_matches_oracle(gpu, oracle, m, n, k, flags, bias, out, dt):
 
 
 @pytest.mark.parametrize("dt", sorted(LP))
-def test_linear_lp_strided_operands(gpu, oracle, dt):
+def test_linear_lp_strided_operands(gpu, oracle, gemm_path, dt):
     """A, W and C as row slices of wider buffers (lda = 96 > k = 40, ldc = 70 > n = 65)."""
     r = np.random.default_rng(3)
     m, n, k = 300, 65, 40
@@ -192,7 +193,7 @@ def test_rms_norm_lp_and_to_lp(gpu, oracle, dt):
 
 @pytest.mark.parametrize("dt", sorted(LP))
 @pytest.mark.parametrize("rows,n,heads,dh,d,dff", [(6, 37, 4, 16, 64, 128), (3, 260, 12, 64, 768, 3072)])
-def test_layer_lp_matches_fp32_oracle(gpu, oracle, rows, n, heads, dh, d, dff, dt):
+def test_layer_lp_matches_fp32_oracle(gpu, oracle, gemm_path, rows, n, heads, dh, d, dff, dt):
     """The bf16/fp16 layer against the fp32 oracle on the unrounded weights and inputs, at the
     bf16/fp16 bar (2e-2)."""
     print(f"case {dt} rows={rows} n={n} heads={heads} dh={dh} d={d} dff={dff}", flush=True)
