@@ -15,6 +15,8 @@
 
 #include <hipblaslt/hipblaslt.h>
 
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <new>
 #include <unordered_map>
@@ -51,10 +53,15 @@ hipDataType hip_type(int dtype) {
 
 }  // namespace
 
+// an activation without a bias runs as activation-with-bias on zeros (x + 0 = x exactly): hipBLASLt
+// has more algorithms for the bias forms
+constexpr int kZeroBias = 1 << 16;
+
 struct Blas {
     hipblasLtHandle_t handle = nullptr;
     void* ws = nullptr;
     size_t ws_bytes = 0;
+    float* zeros = nullptr;  // kZeroBias floats
     std::unordered_map<Key, Entry, KeyHash> cache;
 };
 
@@ -71,6 +78,14 @@ Blas* blas_create() {
         delete b;
         return nullptr;
     }
+    if (hipMalloc(&b->zeros, kZeroBias * sizeof(float)) != hipSuccess ||
+        hipMemset(b->zeros, 0, kZeroBias * sizeof(float)) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
+        (void)hipFree(b->zeros);
+        (void)hipFree(b->ws);
+        (void)hipblasLtDestroy(b->handle);
+        delete b;
+        return nullptr;
+    }
     return b;
 }
 
@@ -83,6 +98,7 @@ void blas_destroy(Blas* b) {
         if (e.la) (void)hipblasLtMatrixLayoutDestroy(e.la);
         if (e.lc) (void)hipblasLtMatrixLayoutDestroy(e.lc);
     }
+    (void)hipFree(b->zeros);
     (void)hipFree(b->ws);
     (void)hipblasLtDestroy(b->handle);
     delete b;
@@ -113,14 +129,19 @@ static Entry* entry_for(Blas* b, const Key& key) {
         hipblasLtMatmulPreference_t pref = nullptr;
         if (hipblasLtMatmulPreferenceCreate(&pref) == 0) {
             const uint64_t wsb = b->ws_bytes;
-            hipblasLtMatmulHeuristicResult_t res[1];
+            constexpr int kAsk = 8;
+            hipblasLtMatmulHeuristicResult_t res[kAsk];
             int got = 0;
             if (hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsb,
                                                       sizeof wsb) == 0 &&
-                hipblasLtMatmulAlgoGetHeuristic(b->handle, e.desc, e.lw, e.la, e.lc, e.lc, pref, 1, res, &got) == 0 &&
-                got > 0 && res[0].workspaceSize <= b->ws_bytes) {
-                e.algo = res[0].algo;
-                e.ok = true;
+                hipblasLtMatmulAlgoGetHeuristic(b->handle, e.desc, e.lw, e.la, e.lc, e.lc, pref, kAsk, res, &got) == 0) {
+                for (int i = 0; i < got; i++) {  // the heuristic's order: the first that fits the workspace
+                    if (res[i].workspaceSize <= b->ws_bytes) {
+                        e.algo = res[i].algo;
+                        e.ok = true;
+                        break;
+                    }
+                }
             }
             (void)hipblasLtMatmulPreferenceDestroy(pref);
         }
@@ -132,21 +153,42 @@ static Entry* entry_for(Blas* b, const Key& key) {
     }
 }
 
+// JITCAST_HIP_BLAS_DEBUG=1 reports on stderr each GEMM shape hipBLASLt declines, once per shape.
+static bool debug_on() {
+    static const bool on = [] {
+        const char* e = getenv("JITCAST_HIP_BLAS_DEBUG");
+        return e && *e == '1';
+    }();
+    return on;
+}
+
+static BlasStatus decline(const char* why, int m, int n, int k, int flags, int ab, int cd) {
+    if (debug_on())
+        fprintf(stderr, "[jc_blas] declined m=%d n=%d k=%d flags=%d ab=%d c=%d: %s\n", m, n, k, flags, ab, cd, why);
+    return kBlasDecline;
+}
+
 BlasStatus blas_gemm(Blas* b, const void* a, int lda, const void* w, const float* bias, void* c, int ldc, int m, int n,
                      int k, int flags, int ab_dtype, int c_dtype, hipStream_t stream) {
     if (!b) return kBlasDecline;
     const bool act = flags & (JC_GEMM_RELU | JC_GEMM_SILU);
     const bool acc = flags & JC_GEMM_ACCUMULATE;
-    if ((act && acc) || c_dtype == JC_F16) return kBlasDecline;
-    if (c_dtype != JC_F32 && c_dtype != ab_dtype) return kBlasDecline;
-    const bool has_bias = (flags & JC_GEMM_BIAS) && bias;
+    if ((act && acc) || c_dtype == JC_F16) return decline("combination", m, n, k, flags, ab_dtype, c_dtype);
+    if (c_dtype != JC_F32 && c_dtype != ab_dtype) return decline("output type", m, n, k, flags, ab_dtype, c_dtype);
+    bool has_bias = (flags & JC_GEMM_BIAS) && bias;
+    if (act && !has_bias) {
+        if (n > kZeroBias) return decline("activation without a bias", m, n, k, flags, ab_dtype, c_dtype);
+        bias = b->zeros;
+        has_bias = true;
+    }
     int epi = HIPBLASLT_EPILOGUE_DEFAULT;
     if (flags & JC_GEMM_RELU) epi = has_bias ? HIPBLASLT_EPILOGUE_RELU_BIAS : HIPBLASLT_EPILOGUE_RELU;
     else if (flags & JC_GEMM_SILU) epi = has_bias ? HIPBLASLT_EPILOGUE_SWISH_BIAS_EXT : HIPBLASLT_EPILOGUE_SWISH_EXT;
     else if (has_bias) epi = HIPBLASLT_EPILOGUE_BIAS;
     const Key key{m, n, k, lda, ldc, ab_dtype, c_dtype, epi, acc ? 1 : 0};
+    const bool fresh = b->cache.find(key) == b->cache.end();
     Entry* e = entry_for(b, key);
-    if (!e || !e->ok) return kBlasDecline;
+    if (!e || !e->ok) return fresh ? decline("no algorithm", m, n, k, flags, ab_dtype, c_dtype) : kBlasDecline;
     if (has_bias &&
         hipblasLtMatmulDescSetAttribute(e->desc, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bias, sizeof bias) != 0)
         return kBlasError;
