@@ -23,7 +23,9 @@
 //     runs.
 // One barrier per block. Wait counts are explicit: every load of the stream is a direct-to-LDS
 // load, loads complete in order among themselves, so waiting until no more than (loads issued
-// after X) are outstanding guarantees X has landed, whatever stores are pending.
+// after X) are outstanding guarantees X has landed, whatever stores are pending. Pending stores
+// still hold such a wait up (the counter counts them too), so an item's output stores go out right
+// after the next step's wait instead of at the end of its last step.
 //
 // The softmax is time_attention_lp.hip's: the key mask and the running max ride in an extra MFMA
 // step, P = exp2(S) rounded to T, v_dot2 row sums, and a wave-uniform slow path for stale maxima.
@@ -648,6 +650,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     int eidx = 0;            // element index within the current item
     bool more = true;
     bool pending = false;    // query 512 of the previous item still to be combined
+    bool fin = false;        // the previous item's tiles still to be written
     int pc_par = 0, pc_r = 0, pc_h = 0;
     while (more) {
         // next compute element (k1, b1) to know whether this one ends its item
@@ -659,8 +662,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
         // query-512 q) right after a step that issued Q loads, those too
         wait_vm_rt(prev_q && (item_start || item_end) ? prev_e : prev_q + prev_e);
         lds_barrier();
-        int r, h;
-        item_rh(ck, r, h);
+        // the previous item's output stores go out here, after this step's wait: s_waitcnt vmcnt
+        // counts stores too, so stores issued at the end of the item would hold up this wait
+        if (fin) finish_item(pc_r, pc_h);
+        fin = false;
         if (pending && wave == kW - 1) reg_combine(pc_par, pc_r, pc_h);
         pending = false;
         if (item_start) {
@@ -686,13 +691,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
         compute(cslot, kmask);
         if (wave < kW / 2) side_work();
         if (item_end) {
-            finish_item(r, h);
+            item_rh(ck, pc_r, pc_h);
+            fin = true;
             if (has_reg) {
                 reg_flush(ck & 1);
                 pending = true;
                 pc_par = ck & 1;
-                pc_r = r;
-                pc_h = h;
             }
         }
         // loads for later: the next item's Q tiles and the query-512 q two items ahead (after this
@@ -721,6 +725,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
         cslot = (cslot + 1) % kSlots;
         more = has_next;
     }
+    if (fin) finish_item(pc_r, pc_h);
     if (pending) {
         lds_barrier();
         if (wave == kW - 1) reg_combine(pc_par, pc_r, pc_h);
