@@ -245,7 +245,7 @@ def layer_line(steps: int, warmup: int, dtype_name: str = "f32") -> dict:
     res = {
         "workload": f"config 4 encoder-layer shape: 1024 groups x (4 series + 1 known covariate), 133 tokens "
                     f"(128 context patches + REG + 4 future), d_model 768, 12x64, d_ff 3072, {dtype_name}",
-        "kernel": "jc_c2_layer (%s for the GEMMs)" % ("jc::gemm_f32" if code == _lib.JC_F32 else "jc::gemm_lp<__bf16>"),
+        "kernel": "jc_c2_layer (hipBLASLt %s GEMMs)" % ("fp32" if code == _lib.JC_F32 else "bf16 x bf16 -> fp32 / bf16"),
         "launch_ms": round(ms, 4),
         "value": round(tf, 2),
         "unit": "TFLOP/s",
@@ -542,6 +542,7 @@ def ts_block_line(steps: int, warmup: int, dtype_name: str = "f32") -> dict:
         "device_forward_ms": round(dev_ms, 2),
         "device_series_per_s": round(rows / (dev_ms * 1e-3), 1),
         "gemm_tflops": round(gemm_flops / (dev_ms * 1e-3) / 1e12, 2),
+        "traffic_per_call": traffic_from_profile(f"ts_block_{dtype_name}_config3"),
     }
     del model
     torch.cuda.empty_cache()
