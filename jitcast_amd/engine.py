@@ -53,7 +53,7 @@ class HipChronos2Engine(ForecastEngine):
         if dtype not in ("f32", "bf16", "fp16"):
             raise ValueError(f"dtype must be f32, bf16 or fp16, got {dtype}")
         device = device if device is not None else opts.integer("jitcast.hip.device", 0, 0)
-        max_plans = max_plans if max_plans is not None else opts.integer("chronos2.hip.plans", 0, 0)
+        max_plans = max_plans if max_plans is not None else opts.integer("chronos2.hip.plans", 8, 0)
         if plan_bytes is None and max_plans > 0:
             import torch
 

@@ -8,8 +8,12 @@ expected; unknown properties are ignored, as the JVM ignores them.
 Properties read by this package:
   chronos2.maxTokens        tokens per forward pass before the pipeline splits it (131072)
   chronos2.hip.dtype        f32 | bf16 | fp16: the encoder's GEMM and time-attention type (f32)
-  chronos2.hip.plans        plans cached per engine, one hipGraph per batch shape; 0 runs eagerly (0)
+  chronos2.hip.plans        plans cached per engine, one hipGraph per batch shape; 0 runs eagerly (8)
   chronos2.hip.planBytes    device bytes the cached plans may hold (the device's memory)
+  timestral.hip.buckets     pad blocks to shared shapes before the forward (true)
+  timestral.hip.plans       plans cached per HipTimestralModel, one hipGraph per block shape; 0 runs
+                            eagerly (8)
+  timestral.hip.planBytes   device bytes those plans may hold (the device's memory)
   jitcast.hip.device        the GPU an engine runs on (0)
 """
 from __future__ import annotations

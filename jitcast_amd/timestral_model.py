@@ -117,13 +117,15 @@ class HipTimestralModel:
     time attention and SwiGLU run in the storage type, the variate attention reads fp32 q|k|v, the
     residual stream, norms' inputs, the embedding and the head stay fp32."""
 
-    def __init__(self, c: TimestralConfig, weights: dict, dtype: str = "f32", device: int = 0, max_plans: int = 0,
-                 plan_bytes: int | None = None, buckets: bool | None = None):
+    def __init__(self, c: TimestralConfig, weights: dict, dtype: str = "f32", device: int = 0,
+                 max_plans: int | None = None, plan_bytes: int | None = None, buckets: bool | None = None):
         """max_plans > 0 runs predict_block's device forward from captured plans, one hipGraph per
         Shape(rows, encoder, horizon, covariates) (TimestralForward.Shape, TimestralForward.java:135),
-        kept in a PlanCache of at most max_plans within plan_bytes of plan buffers (default: no limit);
-        the weights are uploaded once and shared by every plan. buckets (default -Dtimestral.hip.buckets,
-        true) pads each block to a shared shape first (bucketed, TimestralForward.java:81-99, 186-232)."""
+        kept in a PlanCache of at most max_plans within plan_bytes of plan buffers; the weights are
+        uploaded once and shared by every plan. The defaults are the reference's: -Dtimestral.hip.plans
+        (8) and -Dtimestral.hip.planBytes (the device's memory). buckets (default
+        -Dtimestral.hip.buckets, true) pads each block to a shared shape first (bucketed,
+        TimestralForward.java:81-99, 186-232)."""
         import torch
 
         self.c, self.dtype = c, dtype
@@ -148,8 +150,13 @@ class HipTimestralModel:
         self._bufs = {}
         self.buckets = opts.boolean("timestral.hip.buckets", True) if buckets is None else bool(buckets)
         self.plans = None
+        if max_plans is None:
+            max_plans = opts.integer("timestral.hip.plans", 8, 0)
         if max_plans > 0:
-            self.plans = plans_mod.PlanCache(max_plans, plan_bytes if plan_bytes else 1 << 62)
+            if plan_bytes is None:
+                total = torch.cuda.get_device_properties(self.dev).total_memory
+                plan_bytes = opts.bytes_("timestral.hip.planBytes", total, 1)
+            self.plans = plans_mod.PlanCache(max_plans, plan_bytes)
             self._stream = torch.cuda.Stream(self.dev)  # default priority; plans capture and replay on it
 
     def _alloc(self, rows: int, enc: int, h: int, inputs: bool = False) -> dict:

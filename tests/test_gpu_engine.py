@@ -75,6 +75,8 @@ def test_engine_contract(gpu, checkpoint):
     model's levels, close() idempotent and final."""
     eng = HipChronos2Engine.load(checkpoint)
     assert eng.name() == "chronos2-hip"
+    # plans on by default, as the reference's <model>.tornado.plans (8, docs/CONFIGURATION.md:56)
+    assert eng.forward_pass().model.plans.max_plans == 8
     assert eng.config() == C
     s = [TimeSeries.univariate(np.sin(np.arange(200, dtype=np.float32) / 5)),
          TimeSeries([np.ones(90), np.arange(90)], None, [np.linspace(0, 1, 90 + 20)])]

@@ -58,7 +58,7 @@ def test_bucketed_block_forecasts_its_rows_unchanged(gpu, covariates):
 @pytest.mark.parametrize("dt", ["f32", "bf16"])
 def test_planned_blocks_match_eager(gpu, dt):
     print(f"case ts plans {dt}", flush=True)
-    eager = tm.HipTimestralModel(C, _W, dtype=dt, buckets=False)
+    eager = tm.HipTimestralModel(C, _W, dtype=dt, buckets=False, max_plans=0)
     planned = tm.HipTimestralModel(C, _W, dtype=dt, buckets=False, max_plans=2)
     try:
         runs = [(6, 12, 2, False), (9, 7, 1, True), (6, 12, 2, False), (3, 16, 3, False), (6, 12, 2, False)]
@@ -73,3 +73,18 @@ def test_planned_blocks_match_eager(gpu, dt):
     finally:
         planned.close()
     assert planned.plans.keys() == []
+    assert eager.plans is None
+
+
+def test_plans_on_by_default(gpu):
+    """The reference's default: eight plans per model (timestral.tornado.plans, docs/CONFIGURATION.md:131),
+    here -Dtimestral.hip.plans; 0 runs eagerly."""
+    from jitcast_amd import options
+
+    m = tm.HipTimestralModel(C, _W)
+    assert m.plans is not None and m.plans.max_plans == 8
+    options.set_property("timestral.hip.plans", "0")
+    try:
+        assert tm.HipTimestralModel(C, _W).plans is None
+    finally:
+        options.set_property("timestral.hip.plans", None)
