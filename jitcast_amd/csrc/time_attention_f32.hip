@@ -23,6 +23,13 @@
 //
 // K/V/table prefetch uses buffer loads; keys past the end of the row fall outside the resource and
 // read as 0 (and are masked), so the load path has no per-lane bounds branches.
+//
+// FOLD (Chronos-2, rows of 128k + 1 tokens: [REG] after 128k patches): the row's last query would
+// be alone in a fifth workgroup that stages every K/V block for one query. The last full workgroup
+// computes it instead, on VALU beside its MFMA tiles: lane (key 8w + l/8, c = l%8) of wave w takes
+// dims 8c..8c+7 of one key of each 32-key block (8 products and an 8-lane DPP sum give the score),
+// each wave keeps a lazy online softmax over its 8 keys per block and accumulates its share of the
+// output from V^T in LDS, and the four shares are rescaled to a common max once at the end.
 #include "jc_common.hpp"
 #include "jc_kernels.hpp"
 #include "time_mask.hpp"
@@ -45,7 +52,13 @@ struct F32Lds {
     float vt[2][kTiles * 32 * kPitchV];
     uint64_t mask[kMaxTokens / kMaskBlock];  // per 64-key word: key validity bits
     int32_t pos[TS ? kMaxTokens : 1];       // table row of every token of the row (Timestral)
+    float fold_q[DHP];                       // FOLD: the folded query, rotated and scaled
 };
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, (int)kRsrcWord3);
@@ -123,10 +136,11 @@ struct KvStage {
 };
 
 // EXACT: the head is exactly DHP wide, so every head-width expression folds to a constant
-template <int DHP, int KB, bool ROPE, bool TS, bool EXACT>
+template <int DHP, int KB, bool ROPE, bool TS, bool EXACT, bool FOLD>
 __global__ __launch_bounds__(kThreads) void time_attention_f32(const TimeArgs a, int dh_rt) {
     const int dh = EXACT ? DHP : dh_rt;
     static_assert(DHP % 16 == 0 && DHP <= 128, "head width");
+    static_assert(!FOLD || (!TS && EXACT && DHP == 64 && KB == 32), "the folded query: Chronos-2, 64-wide heads");
     static_assert(KB == 32 || KB == 64, "key block");
     constexpr int kHalfP = DHP / 2;
     constexpr int kSteps = kHalfP;  // K=2 per MFMA step: one dim from each lane half
@@ -145,6 +159,7 @@ __global__ __launch_bounds__(kThreads) void time_attention_f32(const TimeArgs a,
     const int qg = logical % a.qgroups;
     const int bh = logical / a.qgroups;
     const int h = bh % a.heads, r = bh / a.heads;
+    const bool fold = FOLD && qg == a.qgroups - 1;  // this workgroup also computes query n - 1
     TimeMask<TS> mask;
     mask.init(a, r);
     const int32_t* vrow = a.valid + (size_t)r * (TS ? a.enc : n);
@@ -194,6 +209,20 @@ __global__ __launch_bounds__(kThreads) void time_attention_f32(const TimeArgs a,
     if (TS) {
         for (int t = tid; t < n; t += kThreads)
             lds.pos[t] = a.pos ? min(max(a.pos[(size_t)r * n + t], 0), a.table_rows - 1) : t;
+    }
+    if (FOLD && fold && wave == 0 && lane < DHP / 2) {
+        // the folded query's dims e and e + 32, rotated at table row n - 1 like the tiles' queries
+        const int qf = n - 1, e = lane;
+        const float* qp = qkv + ((size_t)r * n + qf) * 3 * inner + h * dh;
+        float x = qp[e], y = qp[DHP / 2 + e];
+        if (ROPE) {
+            const float c = a.table[(size_t)qf * dh + e], sn = a.table[(size_t)qf * dh + DHP / 2 + e];
+            const float rx = x * c - y * sn, ry = y * c + x * sn;
+            x = rx;
+            y = ry;
+        }
+        lds.fold_q[e] = x * a.qscale;
+        lds.fold_q[DHP / 2 + e] = y * a.qscale;
     }
     __syncthreads();
     // 64-key words any query of the workgroup can see (the same in every wave)
@@ -250,6 +279,9 @@ __global__ __launch_bounds__(kThreads) void time_attention_f32(const TimeArgs a,
 #pragma unroll
     for (int t = 0; t < kTiles; t++) o_acc[t] = floatx16{0};
     float m_run = -INFINITY, l_run = 0.f;
+    // FOLD: this wave's softmax state for the folded query over its keys (8 per block)
+    float f_m = -INFINITY, f_l = 0.f;
+    floatx4 f_oa = floatx4{0.f, 0.f, 0.f, 0.f}, f_ob = f_oa;
     int buf = 0;
     // Settle every prologue load here: the compiler cannot prove that the divergent Q loads were
     // consumed on all paths and would otherwise wait on them (vmcnt(0)) inside every iteration.
@@ -338,10 +370,102 @@ __global__ __launch_bounds__(kThreads) void time_attention_f32(const TimeArgs a,
                 }
             }
         }
+        if (FOLD && fold) {
+            // the folded query against key 8w + l/8 of the block: dims 8c..8c+7 in this lane
+            const int fkey = 8 * wave + lane / 8, c8 = 8 * (lane % 8);
+            const float* kr = &lds.k[buf][fkey * PK + c8];
+            const floatx4 ka = *reinterpret_cast<const floatx4*>(kr);
+            const floatx4 kb4 = *reinterpret_cast<const floatx4*>(kr + 4);
+            const floatx4 qa4 = *reinterpret_cast<const floatx4*>(&lds.fold_q[c8]);
+            const floatx4 qb4 = *reinterpret_cast<const floatx4*>(&lds.fold_q[c8 + 4]);
+            float sc = 0.f;
+#pragma unroll
+            for (int u = 0; u < 4; u++) sc += ka[u] * qa4[u] + kb4[u] * qb4[u];
+            sc += dpp_f<0xB1>(sc);   // quad_perm [1,0,3,2]
+            sc += dpp_f<0x4E>(sc);   // quad_perm [2,3,0,1]
+            sc += dpp_f<0x141>(sc);  // row_half_mirror: the key's 8 lanes hold its score
+            const bool live = (word >> ((k0 % kMaskBlock) + fkey)) & 1ull;
+            const float fs = live ? sc : -INFINITY;
+            // the reference max moves only when a score passes it by 2^64 (or at the first live key),
+            // so P stays below 2^64
+            if (__any(fs - f_m > 64.f)) {
+                float mx = fmaxf(fs, dpp_f<0x128>(fs));  // row_ror:8: the row's other key
+                auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+                mx = pair_max(fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])));
+                const float m_new = fmaxf(f_m, mx);
+                const float alpha = fast_exp2(f_m - m_new);  // f_m = -inf: 0
+                f_l *= alpha;
+                f_oa *= alpha;
+                f_ob *= alpha;
+                f_m = m_new;
+            }
+            const float p = live ? fast_exp2(fs - f_m) : 0.f;
+            f_l += p;
+            const float* vp = &lds.vt[buf][c8 * PV + fkey];  // V[key][c8 + u] at row c8 + u of V^T
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                f_oa[u] += p * vp[u * PV];
+                f_ob[u] += p * vp[(4 + u) * PV];
+            }
+        }
         if (next < nblk) stage.store(lds, buf ^ 1, tid);
         __syncthreads();
         buf ^= 1;
         kb = next;
+    }
+
+    if (FOLD && fold) {
+        // each wave's share: dims 8c..8c+7 summed over its 8 keys' lanes (c, c+8, ..., c+56), with its
+        // max and sum (each key's P counted in 8 lanes), into the K buffers (free after the loop)
+        floatx4 fo[2] = {f_oa, f_ob};
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                float v = fo[i][u];
+                v += dpp_f<0x128>(v);  // row_ror:8
+                auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+                fo[i][u] = pair_sum(__uint_as_float(sw[0]) + __uint_as_float(sw[1]));
+            }
+        }
+        float lw = f_l;
+        lw += dpp_f<0xB1>(lw);
+        lw += dpp_f<0x4E>(lw);
+        lw += dpp_f<0x124>(lw);  // row_ror:4
+        lw += dpp_f<0x128>(lw);  // row_ror:8
+        {
+            auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(lw), __float_as_uint(lw), false, false);
+            lw = pair_sum(__uint_as_float(sw[0]) + __uint_as_float(sw[1])) * 0.125f;
+        }
+        float* part = &lds.k[0][wave * (DHP + 2)];
+        if (lane < 8) {
+            *reinterpret_cast<floatx4*>(&part[8 * lane]) = fo[0];
+            *reinterpret_cast<floatx4*>(&part[8 * lane + 4]) = fo[1];
+        }
+        if (lane == 0) {
+            part[DHP] = f_m;
+            part[DHP + 1] = lw;
+        }
+        __syncthreads();
+        if (wave == 0) {
+            float mw[kWaves], mx = -INFINITY;
+#pragma unroll
+            for (int w = 0; w < kWaves; w++) {
+                mw[w] = lds.k[0][w * (DHP + 2) + DHP];
+                mx = fmaxf(mx, mw[w]);
+            }
+            float o = 0.f, l = 0.f;
+            if (mx != -INFINITY) {
+#pragma unroll
+                for (int w = 0; w < kWaves; w++) {
+                    const float f = fast_exp2(mw[w] - mx);
+                    o += f * lds.k[0][w * (DHP + 2) + lane];
+                    l += f * lds.k[0][w * (DHP + 2) + DHP + 1];
+                }
+            }
+            float* op = static_cast<float*>(a.out) + ((size_t)r * n + n - 1) * inner + h * dh;
+            op[lane] = l > 0.f ? o / l : 0.f;
+        }
     }
 
     // every lane reaches the swap (its partner holds the other half of the same query)
@@ -376,19 +500,33 @@ __global__ __launch_bounds__(kThreads) void time_attention_f32(const TimeArgs a,
 
 }  // namespace
 
+template <int DHP, int KB, bool TS, bool EXACT, bool FOLD>
+static void launch_f32_rope(const TimeArgs& a, int dh, uint64_t grid, hipStream_t stream) {
+    if (a.table) {
+        hipLaunchKernelGGL((time_attention_f32<DHP, KB, true, TS, EXACT, FOLD>), dim3((uint32_t)grid), dim3(kThreads), 0,
+                           stream, a, dh);
+    } else {
+        hipLaunchKernelGGL((time_attention_f32<DHP, KB, false, TS, EXACT, FOLD>), dim3((uint32_t)grid), dim3(kThreads),
+                           0, stream, a, dh);
+    }
+}
+
 template <int DHP, bool TS, bool EXACT>
 static hipError_t launch_f32(TimeArgs a, int dh, hipStream_t stream) {
     constexpr int KB = 32;  // 32-key blocks (64 measured slower on config 1)
     const int tiles = (a.n + kQ - 1) / kQ;
-    a.qgroups = (tiles + kWaves - 1) / kWaves;
+    // a last query alone after whole workgroups (n = 128k + 1) is folded into the last of them
+    constexpr bool kCanFold = !TS && EXACT && DHP == 64;
+    const bool fold = kCanFold && a.n > 1 && a.n % (kWaves * kQ) == 1;
+    a.qgroups = fold ? (a.n - 1) / (kWaves * kQ) : (tiles + kWaves - 1) / kWaves;
     const uint64_t grid = (uint64_t)a.rows * a.heads * a.qgroups;
-    if (a.table) {
-        hipLaunchKernelGGL((time_attention_f32<DHP, KB, true, TS, EXACT>), dim3((uint32_t)grid), dim3(kThreads), 0,
-                           stream, a, dh);
-    } else {
-        hipLaunchKernelGGL((time_attention_f32<DHP, KB, false, TS, EXACT>), dim3((uint32_t)grid), dim3(kThreads), 0,
-                           stream, a, dh);
+    if constexpr (kCanFold) {
+        if (fold) {
+            launch_f32_rope<DHP, KB, TS, EXACT, true>(a, dh, grid, stream);
+            return hipGetLastError();
+        }
     }
+    launch_f32_rope<DHP, KB, TS, EXACT, false>(a, dh, grid, stream);
     return hipGetLastError();
 }
 

@@ -41,6 +41,8 @@ CASES = [
     (2, 50, 2, 48, 100, "random"),
     (2, 45, 4, 16, 64, "pad"),
     (1, 600, 1, 64, 64, "pad"),
+    (2, 257, 2, 64, 128, "random"),
+    (1, 129, 2, 64, 128, "all"),
 ]
 
 
@@ -175,8 +177,9 @@ def test_bf16_config1_shape_subset_matches_oracle(gpu, oracle, lp_kernel):
     assert err <= TOL_LP
 
 
-def test_fp32_no_live_key_gives_zeros(gpu, oracle):
-    rows, n, heads, dh, inner = 3, 40, 2, 64, 128
+@pytest.mark.parametrize("n", [40, 129])
+def test_fp32_no_live_key_gives_zeros(gpu, oracle, n):
+    rows, heads, dh, inner = 3, 2, 64, 128
     qkv = cases.qkv(29, rows * n, inner)
     live = cases.left_pad_live(29, rows, n, 10)
     live[1] = 0
@@ -186,21 +189,40 @@ def test_fp32_no_live_key_gives_zeros(gpu, oracle):
     assert oracle.rel_max_error(got, exp) <= TOL_F32
 
 
-def test_fp32_one_live_key_returns_its_value(gpu):
-    rows, n, heads, dh, inner = 2, 70, 2, 64, 128
+@pytest.mark.parametrize("n", [70, 129])
+def test_fp32_one_live_key_returns_its_value(gpu, n):
+    rows, heads, dh, inner = 2, 2, 64, 128
     qkv = cases.qkv(31, rows * n, inner)
     live = np.zeros((rows, n), np.int32)
     live[0, 3] = 1
-    live[1, 69] = 1
+    live[1, n - 1] = 1
     got = _run(qkv, live, rows, n, heads, dh, inner).reshape(rows, n, inner)
     v = qkv.reshape(rows, n, 3 * inner)[:, :, 2 * inner:]
     np.testing.assert_allclose(got[0], np.broadcast_to(v[0, 3], (n, inner)), rtol=1e-6, atol=1e-6)
-    np.testing.assert_allclose(got[1], np.broadcast_to(v[1, 69], (n, inner)), rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(got[1], np.broadcast_to(v[1, n - 1], (n, inner)), rtol=1e-6, atol=1e-6)
 
 
-def test_fp32_without_table_is_plain_attention(gpu):
+@pytest.mark.parametrize("n,kind", [(129, "pad"), (257, "random"), (513, "pad")])
+def test_fp32_folded_last_query(gpu, oracle, n, kind):
+    """Rows of 128k + 1 tokens: the last query ([REG]) is computed by the last full workgroup on VALU
+    instead of a workgroup of its own. Its output is checked on its own, per head, besides the whole."""
+    rows, heads, dh, inner = 3, 3, 64, 200
+    print(f"case folded n={n} {kind}", flush=True)
+    qkv = cases.qkv(41, rows * n, inner)
+    live = _live(kind, 41, rows, n)
+    got = _run(qkv, live, rows, n, heads, dh, inner).reshape(rows, n, inner)
+    exp = oracle.c2_time_attention(qkv, live, rows, n, heads, dh, inner).reshape(rows, n, inner)
+    assert oracle.rel_max_error(got[:, :, : heads * dh], exp[:, :, : heads * dh]) <= TOL_F32
+    for h in range(heads):
+        sl = np.s_[:, n - 1, h * dh:(h + 1) * dh]
+        assert oracle.rel_max_error(got[sl], exp[sl]) <= TOL_F32, h
+    assert np.isnan(got[:, :, heads * dh:]).all(), "columns past heads * dh are not written"
+
+
+@pytest.mark.parametrize("n", [65, 129])
+def test_fp32_without_table_is_plain_attention(gpu, n):
     """rope_table NULL: qkv is taken as already rotated (the reference's separate rope task ran)."""
-    rows, n, heads, dh, inner = 2, 65, 2, 64, 128
+    rows, heads, dh, inner = 2, 2, 64, 128
     qkv = cases.qkv(37, rows * n, inner)
     live = cases.left_pad_live(37, rows, n, 30)
     got = _run(qkv, live, rows, n, heads, dh, inner, table=False)
