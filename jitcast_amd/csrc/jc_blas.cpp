@@ -20,6 +20,7 @@
 #include <cstring>
 #include <new>
 #include <unordered_map>
+#include <unordered_set>
 
 #include "../../include/jitcast_hip.h"
 
@@ -63,6 +64,7 @@ struct Blas {
     size_t ws_bytes = 0;
     float* zeros = nullptr;  // kZeroBias floats
     std::unordered_map<Key, Entry, KeyHash> cache;
+    std::unordered_set<uint64_t> reported;  // declined shapes already reported (JITCAST_HIP_BLAS_DEBUG)
 };
 
 Blas* blas_create() {
@@ -153,7 +155,7 @@ static Entry* entry_for(Blas* b, const Key& key) {
     }
 }
 
-// JITCAST_HIP_BLAS_DEBUG=1 reports on stderr each GEMM shape hipBLASLt declines, once per shape.
+// JITCAST_HIP_BLAS_DEBUG=1 reports on stderr each GEMM shape this path declines, once per shape and context.
 static bool debug_on() {
     static const bool on = [] {
         const char* e = getenv("JITCAST_HIP_BLAS_DEBUG");
@@ -162,9 +164,18 @@ static bool debug_on() {
     return on;
 }
 
-static BlasStatus decline(const char* why, int m, int n, int k, int flags, int ab, int cd) {
-    if (debug_on())
-        fprintf(stderr, "[jc_blas] declined m=%d n=%d k=%d flags=%d ab=%d c=%d: %s\n", m, n, k, flags, ab, cd, why);
+static BlasStatus decline(Blas* b, const char* why, int m, int n, int k, int flags, int ab, int cd) {
+    if (debug_on()) {
+        uint64_t h = 1469598103934665603ull;
+        for (int v : {m, n, k, flags, ab, cd}) h = (h ^ (uint32_t)v) * 1099511628211ull;
+        bool fresh = true;
+        try {
+            fresh = b->reported.insert(h).second;
+        } catch (...) {
+        }
+        if (fresh)
+            fprintf(stderr, "[jc_blas] declined m=%d n=%d k=%d flags=%d ab=%d c=%d: %s\n", m, n, k, flags, ab, cd, why);
+    }
     return kBlasDecline;
 }
 
@@ -173,11 +184,11 @@ BlasStatus blas_gemm(Blas* b, const void* a, int lda, const void* w, const float
     if (!b) return kBlasDecline;
     const bool act = flags & (JC_GEMM_RELU | JC_GEMM_SILU);
     const bool acc = flags & JC_GEMM_ACCUMULATE;
-    if ((act && acc) || c_dtype == JC_F16) return decline("combination", m, n, k, flags, ab_dtype, c_dtype);
-    if (c_dtype != JC_F32 && c_dtype != ab_dtype) return decline("output type", m, n, k, flags, ab_dtype, c_dtype);
+    if ((act && acc) || c_dtype == JC_F16) return decline(b, "combination", m, n, k, flags, ab_dtype, c_dtype);
+    if (c_dtype != JC_F32 && c_dtype != ab_dtype) return decline(b, "output type", m, n, k, flags, ab_dtype, c_dtype);
     bool has_bias = (flags & JC_GEMM_BIAS) && bias;
     if (act && !has_bias) {
-        if (n > kZeroBias) return decline("activation without a bias", m, n, k, flags, ab_dtype, c_dtype);
+        if (n > kZeroBias) return decline(b, "activation without a bias", m, n, k, flags, ab_dtype, c_dtype);
         bias = b->zeros;
         has_bias = true;
     }
@@ -186,9 +197,8 @@ BlasStatus blas_gemm(Blas* b, const void* a, int lda, const void* w, const float
     else if (flags & JC_GEMM_SILU) epi = has_bias ? HIPBLASLT_EPILOGUE_SWISH_BIAS_EXT : HIPBLASLT_EPILOGUE_SWISH_EXT;
     else if (has_bias) epi = HIPBLASLT_EPILOGUE_BIAS;
     const Key key{m, n, k, lda, ldc, ab_dtype, c_dtype, epi, acc ? 1 : 0};
-    const bool fresh = b->cache.find(key) == b->cache.end();
     Entry* e = entry_for(b, key);
-    if (!e || !e->ok) return fresh ? decline("no algorithm", m, n, k, flags, ab_dtype, c_dtype) : kBlasDecline;
+    if (!e || !e->ok) return decline(b, "no algorithm", m, n, k, flags, ab_dtype, c_dtype);
     if (has_bias &&
         hipblasLtMatmulDescSetAttribute(e->desc, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bias, sizeof bias) != 0)
         return kBlasError;

@@ -155,7 +155,7 @@ def _oracle_forecast(oracle, c, w, lay):
     return oracle.c2_finish(raw, loc, scale, lay.rows, lay.h, c.num_quantiles, c.patch_size, c.use_arcsinh)
 
 
-@pytest.mark.parametrize("dt", ["f32", "bf16"])
+@pytest.mark.parametrize("dt", ["f32", "bf16", "fp16"])
 def test_config4_forecast_matches_oracle(gpu, oracle, dt):
     groups, h = 2, 4
     print(f"case config 4 forecast {dt}: {groups} groups x 5 rows x 2048 steps, h={h}, 120M-class", flush=True)
