@@ -211,16 +211,25 @@ def layer_line(steps: int, warmup: int, dtype_name: str = "f32") -> dict:
     """Config 4's encoder-layer shape through jc_c2_layer: RMSNorm, the six GEMMs of the layer, RoPE
     time attention, group attention, ReLU and the residual adds. f32: everything fp32. bf16: the
     GEMMs and the time attention in bf16 with fp32 accumulation (weights converted once, outside the
-    timed region), the group attention, norms and residual stream fp32."""
+    timed region), the group attention, norms and residual stream fp32. f16x3: f32's layer with every
+    GEMM on three-term fp16 splits of its operands (weights split once, outside the timed region)."""
     import torch
 
     from jitcast_amd import _lib, chronos2, synthetic
 
     case = synthetic.c2_layer_config4(device="cuda")
-    code = {"f32": _lib.JC_F32, "bf16": _lib.JC_BF16}[dtype_name]
+    code = {"f32": _lib.JC_F32, "bf16": _lib.JC_BF16, "f16x3": _lib.JC_F16X3}[dtype_name]
     weights = dict(case.weights)
     ws = case.workspace
-    if code != _lib.JC_F32:
+    if code == _lib.JC_F16X3:
+        for k in ("time_qkv", "time_o", "group_qkv", "group_o", "wi", "wo"):
+            x3 = torch.empty(weights[k].shape[0], 3 * weights[k].shape[1], dtype=torch.float16, device="cuda")
+            chronos2.split_f16x3(weights[k].contiguous(), x3, weights=True)
+            weights[k] = x3
+        inner = case.heads * case.dh
+        ws = torch.empty(chronos2.layer_workspace_bytes(case.rows, case.n, case.d, inner, case.dff, code) // 4 + 64,
+                         dtype=torch.float32, device="cuda")
+    elif code != _lib.JC_F32:
         for k in ("time_qkv", "time_o", "group_qkv", "group_o", "wi", "wo"):
             lp = torch.empty(weights[k].shape, dtype=torch.bfloat16, device="cuda")
             chronos2.to_lp(weights[k], lp)
@@ -238,6 +247,8 @@ def layer_line(steps: int, warmup: int, dtype_name: str = "f32") -> dict:
     case.x.copy_(x0)
     flops = case.flops()
     tf = flops / (ms * 1e-3) / 1e12
+    # f16x3 runs its GEMMs on fp16 MFMA, three products per fp32 product: it is priced against the fp16
+    # peak with the algorithmic (fp32) flops, and the executed MFMA flops are reported beside them
     peak = PEAK_FP32_TFLOPS if code == _lib.JC_F32 else PEAK_BF16_TFLOPS
     tokens = case.rows * case.n
     log(f"layer {dtype_name}: {ms:.3f} ms, {tf:.1f} TFLOP/s ({100 * tf / peak:.1f}% of the {dtype_name} MFMA peak), "
@@ -245,7 +256,8 @@ def layer_line(steps: int, warmup: int, dtype_name: str = "f32") -> dict:
     res = {
         "workload": f"config 4 encoder-layer shape: 1024 groups x (4 series + 1 known covariate), 133 tokens "
                     f"(128 context patches + REG + 4 future), d_model 768, 12x64, d_ff 3072, {dtype_name}",
-        "kernel": "jc_c2_layer (hipBLASLt %s GEMMs)" % ("fp32" if code == _lib.JC_F32 else "bf16 x bf16 -> fp32 / bf16"),
+        "kernel": "jc_c2_layer (hipBLASLt %s GEMMs)" % {_lib.JC_F32: "fp32", _lib.JC_BF16: "bf16 x bf16 -> fp32 / bf16",
+                                                         _lib.JC_F16X3: "fp16 GEMMs over three-term splits, K = 3k"}[code],
         "launch_ms": round(ms, 4),
         "value": round(tf, 2),
         "unit": "TFLOP/s",
@@ -256,6 +268,8 @@ def layer_line(steps: int, warmup: int, dtype_name: str = "f32") -> dict:
         "flops_per_step": flops,
         "gemm_share_of_flops": round(case.gemm_flops() / flops, 4),
     }
+    if code == _lib.JC_F16X3:
+        res["executed_tflops"] = round((flops + 2 * case.gemm_flops()) / (ms * 1e-3) / 1e12, 2)
     del case, x0, weights, ws
     torch.cuda.empty_cache()
     return res
@@ -556,7 +570,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=256)
-    ap.add_argument("--only", choices=["all", "time", "group", "bf16", "fp16", "layer", "layer-bf16", "ts", "ts-block", "ts-block-bf16", "forecast"], default="all",
+    ap.add_argument("--only", choices=["all", "time", "group", "bf16", "fp16", "layer", "layer-bf16", "layer-f16x3", "ts", "ts-block", "ts-block-bf16", "forecast"], default="all",
                     help="which workloads to run (profiling runs select one kernel)")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="only run 5 plain device copies of this many bytes (calibrates rocprof byte counters)")
@@ -599,6 +613,8 @@ def main() -> int:
             series, n_targets = c4_series()
             # fp32 first: the encoder inside config 4's 1e-3 quantile bar
             also["c2_forecast_f32"] = forecast_line(ckpt, series, n_targets, "f32", cpu=want_cpu)
+            # f16x3: fp16 GEMMs over three-term splits, inside the same 1e-3 bar
+            also["c2_forecast_f16x3"] = forecast_line(ckpt, series, n_targets, "f16x3")
             also["c2_forecast_bf16"] = forecast_line(ckpt, series, n_targets, "bf16")
         finally:
             shutil.rmtree(ckpt, ignore_errors=True)
@@ -616,9 +632,10 @@ def main() -> int:
         if args.only == "ts":
             print(json.dumps({"also": also}), flush=True)
             return 0
-    if args.only in ("all", "layer-bf16"):
-        also["c2_layer_bf16"] = layer_line(max(3, args.steps // 5), 1, "bf16")
-        if args.only == "layer-bf16":
+    if args.only in ("all", "layer-bf16", "layer-f16x3"):
+        for name in (("bf16", "f16x3") if args.only == "all" else (args.only[6:],)):
+            also[f"c2_layer_{name}"] = layer_line(max(3, args.steps // 5), 1, name)
+        if args.only != "all":
             print(json.dumps({"also": also}), flush=True)
             return 0
     if args.only in ("all", "layer"):

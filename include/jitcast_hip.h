@@ -41,7 +41,9 @@ typedef enum jc_status {
 typedef enum jc_dtype {
     JC_F32 = 0,  /* fp32 in and out, fp32 MFMA: the reference's FP32-exact default */
     JC_BF16 = 1, /* bf16 qkv and out, bf16 MFMA with fp32 accumulation and fp32 softmax */
-    JC_F16 = 2   /* fp16 qkv and out (saturated to +-65504 as Kernels.java:42-46), fp32 accumulation */
+    JC_F16 = 2,  /* fp16 qkv and out (saturated to +-65504 as Kernels.java:42-46), fp32 accumulation */
+    JC_F16X3 = 3 /* jc_c2_layer only: fp32 in and out, each GEMM as three fp16 products with fp32
+                    accumulation (jc_split_f16x3), about fp32's accuracy; no reference counterpart */
 } jc_dtype;
 
 typedef struct jc_ctx jc_ctx;
@@ -286,9 +288,21 @@ int jc_linear(jc_ctx *ctx, const float *a, int lda, const float *w, const float 
  */
 int jc_rms_norm(jc_ctx *ctx, const float *x, const float *w, float *y, int rows, int d, float eps);
 
+/*
+ * The three-term fp16 split of an fp32 matrix src [rows, ld_src] (k columns): dst [rows, 3k] fp16
+ * holds, per row, [hi | hi | lo] (weights = 0: a GEMM's A operand) or [hi | lo | hi] (weights = 1:
+ * its W operand), hi = fp16(v) saturated to +-65504, lo = fp16(v - hi). One fp16 GEMM over K = 3k
+ * with fp32 accumulation then sums a_hi w_hi + a_hi w_lo + a_lo w_hi: each product within about
+ * 2^-20 |a w| + 2^-25 (|a| + |w|) (hi + lo = v within 2^-22 |v| + 2^-25; hi saturates beyond
+ * +-65504, as the FP16 GEMM mode's operands do). No counterpart in the reference: it is the JC_F16X3 layer's operand format (fp32
+ * accuracy on fp16 MFMA). k and ld_src multiples of 4, src 16-byte aligned, dst 8-byte aligned.
+ */
+int jc_split_f16x3(jc_ctx *ctx, const float *src, int ld_src, void *dst, int rows, int k, int weights);
+
 /* Device weights of one Chronos-2 encoder layer (Chronos2Packed.Layer, Chronos2Packed.java:41-47,
- * 150-154). The matrices are fp32 for a JC_F32 layer and bf16 / fp16 for a JC_BF16 / JC_F16 layer
- * (jc_to_lp converts them once); norm weights and biases are always fp32. A bias may be NULL. */
+ * 150-154). The matrices are fp32 for a JC_F32 layer, bf16 / fp16 for a JC_BF16 / JC_F16 layer
+ * (jc_to_lp converts them once) and fp16 [n, 3k] W-operand splits for a JC_F16X3 layer
+ * (jc_split_f16x3 with weights = 1); norm weights and biases are always fp32. A bias may be NULL. */
 typedef struct jc_c2_layer_weights {
     const float *time_norm;  /* [d] */
     const void *time_qkv;    /* [3*inner, d]: q | k | v rows, heads-major */
@@ -310,7 +324,9 @@ typedef struct jc_c2_layer_weights {
 /* Bytes of the workspace jc_c2_layer needs for T = rows*n tokens, each part 256-byte aligned, or
  * -1 for a negative size. JC_F32: hn [T, d], big [T, max(3*inner, dff)], att [T, inner] floats.
  * JC_BF16 / JC_F16: hn [T, d] and att [T, inner] in the storage type, big [T, max(3*inner floats,
- * dff storage values)] and an fp32 att [T, inner] for the group attention. */
+ * dff storage values)] and an fp32 att [T, inner] for the group attention. JC_F16X3: big
+ * [T, max(3*inner, dff)] and att [T, inner] floats and the split operand [T, 3*max(d, inner, dff)]
+ * fp16. */
 int64_t jc_c2_layer_workspace_bytes(int rows, int n, int d, int inner, int dff, int dtype);
 
 /*
@@ -327,7 +343,11 @@ int64_t jc_c2_layer_workspace_bytes(int rows, int n, int d, int inner, int dff, 
  * dtype JC_F32: everything in fp32. JC_BF16 / JC_F16: the GEMMs take the storage type with fp32
  * accumulation (the reference's FP16 GEMM modes, Chronos2Forward.java:377-409, GemmMode.HALF), the
  * time attention runs in the storage type, the group attention in fp32, and x (the residual
- * stream), the norms and the accumulations stay fp32.
+ * stream), the norms and the accumulations stay fp32. JC_F16X3 (no reference counterpart): every
+ * GEMM runs on its operands' three-term fp16 splits (jc_split_f16x3; the norms write the split
+ * directly), with fp32 accumulation and fp32 outputs; the attention, the norms and x are fp32, as in
+ * JC_F32, whose accuracy it keeps to about 2^-20 per product (plus 2^-25 times the other operand
+ * where lo is subnormal, for operands below about 2^-2).
  */
 int jc_c2_layer(jc_ctx *ctx, float *x, const jc_c2_layer_weights *w, const int32_t *live, const float *table,
                 const int32_t *group_start, const int32_t *group_end, void *workspace, int rows, int n, int d,

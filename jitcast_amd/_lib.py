@@ -15,7 +15,7 @@ LIB_PATH = HERE / "libjitcast_hip.so"
 HEADER = HERE.parent / "include" / "jitcast_hip.h"
 
 JC_OK, JC_EINVAL, JC_EHIP, JC_ENOMEM, JC_EUNSUPPORTED, JC_ESTATE = 0, -1, -2, -3, -4, -5
-JC_F32, JC_BF16, JC_F16 = 0, 1, 2
+JC_F32, JC_BF16, JC_F16, JC_F16X3 = 0, 1, 2, 3
 
 
 class LibraryMissing(ImportError):
@@ -80,6 +80,7 @@ SIGNATURES = {
     "jc_linear_lp": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i]),
     "jc_rms_norm_lp": (_i, [_vp, _vp, _vp, _vp, _i, _i, _f, _i]),
     "jc_to_lp": (_i, [_vp, _vp, _vp, _c.c_int64, _i]),
+    "jc_split_f16x3": (_i, [_vp, _vp, _i, _vp, _i, _i, _i]),
     "jc_c2_assemble": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i]),
     "jc_c2_gather_future": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i]),
     "jc_ts_residual": (_i, [_vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp]),

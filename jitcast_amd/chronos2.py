@@ -164,7 +164,9 @@ def layer(x, weights: dict, live, table, group_start, group_end, workspace, rows
 
     dtype JC_F32: fp32 weights. JC_BF16 / JC_F16: the weight matrices in that type (to_lp converts
     them), norm weights and biases fp32; GEMMs and time attention in the storage type with fp32
-    accumulation, the residual stream fp32."""
+    accumulation, the residual stream fp32. JC_F16X3: the weight matrices as fp16 [n, 3k] W-operand
+    splits (split_f16x3 with weights=True); each GEMM product within about 2^-20 |a w| +
+    2^-25 (|a| + |w|), fp32 accumulation and outputs."""
     _f32(x, "x")
     ctx = context(x.device.index or 0)
     lw = LayerWeights.of(weights)
@@ -211,6 +213,19 @@ def rms_norm_lp(x, w, y, eps: float) -> None:
     ctx = context(x.device.index or 0)
     rows, d = x.shape
     _lib.call("jc_rms_norm_lp", ctx.handle, _ptr(x), _ptr(w), _ptr(y), rows, d, ctypes.c_float(eps), _dtype_code(y))
+
+
+def split_f16x3(src, dst, weights: bool = False) -> None:
+    """dst float16 [rows, 3k] = the three-term split of src float32 [rows, k] (jc_split_f16x3):
+    [hi | hi | lo] per row, or [hi | lo | hi] with weights, hi = fp16(v) saturated, lo = fp16(v - hi)."""
+    _f32(src, "src")
+    if src.dim() != 2 or dst.dim() != 2 or dst.shape[0] != src.shape[0] or dst.shape[1] != 3 * src.shape[1]:
+        raise _lib.JitcastArgumentError(_lib.JC_EINVAL, "split_f16x3: src [rows, k] and dst [rows, 3k]")
+    if _dtype_code(dst) != _lib.JC_F16:
+        raise _lib.JitcastArgumentError(_lib.JC_EINVAL, "split_f16x3: dst must be float16")
+    ctx = context(src.device.index or 0)
+    _lib.call("jc_split_f16x3", ctx.handle, _ptr(src), src.stride(0), _ptr(dst), src.shape[0], src.shape[1],
+              1 if weights else 0)
 
 
 def to_lp(src, dst) -> None:

@@ -220,7 +220,9 @@ class HipChronos2Model:
     """The Chronos-2 forward on one GPU: weights uploaded once; per call the host prep, one upload,
     the device forward, one download and the host finish. dtype "f32" runs every layer in fp32;
     "bf16"/"fp16" runs the encoder layers' GEMMs and time attention in that type with fp32
-    accumulation (the reference's FP16 GEMM mode), the embeddings and head in fp32."""
+    accumulation (the reference's FP16 GEMM mode), the embeddings and head in fp32; "f16x3" runs the
+    layers' GEMMs on three-term fp16 splits of their operands (fp32 accumulation and outputs, about
+    fp32's accuracy) and everything else as "f32"."""
 
     def __init__(self, c: Chronos2Config, weights: dict, dtype: str = "f32", device: int = 0, max_plans: int = 0,
                  plan_bytes: int | None = None):
@@ -232,7 +234,7 @@ class HipChronos2Model:
         import torch
 
         self.c, self.dtype = c, dtype
-        self.code = {"f32": _lib.JC_F32, "bf16": _lib.JC_BF16, "fp16": _lib.JC_F16}[dtype]
+        self.code = {"f32": _lib.JC_F32, "bf16": _lib.JC_BF16, "fp16": _lib.JC_F16, "f16x3": _lib.JC_F16X3}[dtype]
         self.dev = torch.device("cuda", device)
         t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(self.dev)  # noqa: E731
         self.w = {k: t(v) for k, v in weights.items() if k != "layers"}
@@ -240,7 +242,13 @@ class HipChronos2Model:
         self.layers = []
         for lw in weights["layers"]:
             d = {k: t(v) for k, v in lw.items()}
-            if self.code != _lib.JC_F32:
+            if self.code == _lib.JC_F16X3:
+                for k in ("time_qkv", "time_o", "group_qkv", "group_o", "wi", "wo"):
+                    src = d[k].contiguous()
+                    x3 = torch.empty(src.shape[0], 3 * src.shape[1], dtype=torch.float16, device=self.dev)
+                    chronos2.split_f16x3(src, x3, weights=True)
+                    d[k] = x3
+            elif self.code != _lib.JC_F32:
                 tdt = {_lib.JC_BF16: torch.bfloat16, _lib.JC_F16: torch.float16}[self.code]
                 for k in ("time_qkv", "time_o", "group_qkv", "group_o", "wi", "wo"):
                     lp = torch.empty(d[k].shape, dtype=tdt, device=self.dev)

@@ -688,6 +688,12 @@ int64_t jc_c2_layer_workspace_bytes(int rows, int n, int d, int inner, int dff, 
         const size_t big = (size_t)(3 * inner > dff ? 3 * inner : dff);
         return (int64_t)(round256(t * d * 4) + round256(t * big * 4) + round256(t * (size_t)inner * 4));
     }
+    if (dtype == JC_F16X3) {
+        const size_t big = (size_t)(3 * inner > dff ? 3 * inner : dff);
+        size_t wide = (size_t)(d > inner ? d : inner);
+        if ((size_t)dff > wide) wide = (size_t)dff;
+        return (int64_t)(round256(t * big * 4) + round256(t * (size_t)inner * 4) + round256(t * 3 * wide * 2));
+    }
     if (dtype != JC_BF16 && dtype != JC_F16) return -1;
     const size_t big = (size_t)(12 * inner > 2 * dff ? 12 * inner : 2 * dff);  // bytes per token
     return (int64_t)(round256(t * d * 2) + round256(t * big) + round256(t * (size_t)inner * 4) +
@@ -697,6 +703,9 @@ int64_t jc_c2_layer_workspace_bytes(int rows, int n, int d, int inner, int dff, 
 static int layer_lp(jc_ctx* ctx, const char* W, float* x, const jc_c2_layer_weights* w, const int32_t* live,
                     const float* table, const int32_t* group_start, const int32_t* group_end, void* workspace, int rows,
                     int n, int d, int heads, int dh, int dff, float eps, int dtype);
+static int layer_x3(jc_ctx* ctx, const char* W, float* x, const jc_c2_layer_weights* w, const int32_t* live,
+                    const float* table, const int32_t* group_start, const int32_t* group_end, void* workspace, int rows,
+                    int n, int d, int heads, int dh, int dff, float eps);
 
 static int c2_layer(jc_ctx* ctx, const char* W, float* x, const jc_c2_layer_weights* w, const int32_t* live,
                     const float* table, const int32_t* group_start, const int32_t* group_end, void* workspace, int rows,
@@ -718,7 +727,10 @@ static int c2_layer(jc_ctx* ctx, const char* W, float* x, const jc_c2_layer_weig
     if (dtype == JC_BF16 || dtype == JC_F16)
         return layer_lp(ctx, W, x, w, live, table, group_start, group_end, workspace, rows, n, d, heads, dh, dff, eps,
                         dtype);
-    if (dtype != JC_F32) return fail(JC_EINVAL, "%s: dtype must be JC_F32, JC_BF16 or JC_F16 (got %d)", W, dtype);
+    if (dtype == JC_F16X3)
+        return layer_x3(ctx, W, x, w, live, table, group_start, group_end, workspace, rows, n, d, heads, dh, dff, eps);
+    if (dtype != JC_F32)
+        return fail(JC_EINVAL, "%s: dtype must be JC_F32, JC_BF16, JC_F16 or JC_F16X3 (got %d)", W, dtype);
     const int inner = heads * dh, T = rows * n;
     const size_t big_cols = (size_t)(3 * inner > dff ? 3 * inner : dff);
     char* ws = static_cast<char*>(workspace);
@@ -763,7 +775,7 @@ int jc_c2_layer_static(jc_ctx* ctx, float* x, const jc_c2_layer_weights* w, cons
                     heads, dh, dff);
     if ((int64_t)heads * dh > INT32_MAX / 12) return fail(JC_EINVAL, "%s: heads * dh too large", W);
     const int64_t need = jc_c2_layer_workspace_bytes(rows, n, d, heads * dh, dff, dtype);
-    if (need < 0) return fail(JC_EINVAL, "%s: dtype must be JC_F32, JC_BF16 or JC_F16 (got %d)", W, dtype);
+    if (need < 0) return fail(JC_EINVAL, "%s: dtype must be JC_F32, JC_BF16, JC_F16 or JC_F16X3 (got %d)", W, dtype);
     if (need > (int64_t)JC_C2_LAYER_STATIC_BYTES)
         return fail(JC_EINVAL,
                     "%s: %d rows x %d tokens need %lld bytes of workspace, past the %lld-byte static scratch "
@@ -901,6 +913,75 @@ static int layer_lp(jc_ctx* ctx, const char* W, float* x, const jc_c2_layer_weig
     if ((rc = launch_linear_lp(ctx, W, hn, d, w->wi, w->wi_bias, big, dff, T, dff, d, JC_GEMM_RELU, dtype, dtype)))
         return rc;
     return launch_linear_lp(ctx, W, big, dff, w->wo, w->wo_bias, x, d, T, d, dff, JC_GEMM_ACCUMULATE, dtype, JC_F32);
+}
+
+// ---- fp32 layer on fp16 operand splits (JC_F16X3) ------------------------------------------------
+
+static int launch_split_x3(jc_ctx* ctx, const char* W, const float* src, int ld, void* dst, int rows, int k,
+                           int weights) {
+    if (rows < 0 || k < 0) return fail(JC_EINVAL, "%s: negative size (rows=%d k=%d)", W, rows, k);
+    if ((size_t)rows * k == 0) return JC_OK;
+    if (!src || !dst) return fail(JC_EINVAL, "%s: null src or dst", W);
+    if (k % 4 || ld < k || ld % 4) return fail(JC_EINVAL, "%s: k and ld must be multiples of 4, ld >= k (k=%d ld=%d)", W, k, ld);
+    if (!aligned16(src) || ((uintptr_t)dst & 7u)) return fail(JC_EINVAL, "%s: src 16-byte and dst 8-byte alignment", W);
+    if (weights != 0 && weights != 1) return fail(JC_EINVAL, "%s: weights must be 0 or 1 (got %d)", W, weights);
+    hipError_t e = jc::split_x3_launch(src, ld, dst, rows, k, weights == 1, ctx->stream);
+    return e == hipSuccess ? JC_OK : hip_fail(W, e);
+}
+
+int jc_split_f16x3(jc_ctx* ctx, const float* src, int ld_src, void* dst, int rows, int k, int weights) {
+    const char* W = "jc_split_f16x3";
+    int rc = use(ctx, W);
+    if (rc) return rc;
+    return launch_split_x3(ctx, W, src, ld_src, dst, rows, k, weights);
+}
+
+// The JC_F32 layer with every GEMM on the operands' three-term fp16 splits: the norms write the
+// A-operand split of hn directly, the attention outputs and the MLP activation are split before their
+// GEMMs, and every GEMM (K = 3k, fp32 accumulation) writes fp32.
+static int layer_x3(jc_ctx* ctx, const char* W, float* x, const jc_c2_layer_weights* w, const int32_t* live,
+                    const float* table, const int32_t* group_start, const int32_t* group_end, void* workspace, int rows,
+                    int n, int d, int heads, int dh, int dff, float eps) {
+    const int inner = heads * dh, T = rows * n;
+    const size_t t = (size_t)T;
+    const size_t big_cols = (size_t)(3 * inner > dff ? 3 * inner : dff);
+    char* ws = static_cast<char*>(workspace);
+    float* big = reinterpret_cast<float*>(ws);                                  // qkv [T, 3*inner] or act [T, dff]
+    float* att = reinterpret_cast<float*>(ws + round256(t * big_cols * 4));    // [T, inner]
+    void* a3 = ws + round256(t * big_cols * 4) + round256(t * (size_t)inner * 4);  // [T, 3k] fp16, k <= max(d, inner, dff)
+    const int F = JC_F16;
+    int rc;
+    auto rms3 = [&](const float* nw) -> int {
+        hipError_t e = jc::rms_norm_x3_launch(x, a3, nw, T, d, eps, ctx->stream);
+        return e == hipSuccess ? JC_OK : hip_fail(W, e);
+    };
+    // time attention sub-layer (Chronos2Forward.java:260-271)
+    if ((rc = rms3(w->time_norm))) return rc;
+    if ((rc = launch_linear_lp(ctx, W, a3, 3 * d, w->time_qkv, w->time_qkv_bias, big, 3 * inner, T, 3 * inner, 3 * d, 0,
+                               F, JC_F32)))
+        return rc;
+    if ((rc = jc_c2_time_attention(ctx, big, att, live, table, rows, n, heads, dh, inner, JC_F32))) return rc;
+    if ((rc = launch_split_x3(ctx, W, att, inner, a3, T, inner, 0))) return rc;
+    if ((rc = launch_linear_lp(ctx, W, a3, 3 * inner, w->time_o, w->time_o_bias, x, d, T, d, 3 * inner,
+                               JC_GEMM_ACCUMULATE, F, JC_F32)))
+        return rc;
+    // group attention sub-layer (Chronos2Forward.java:273-281)
+    if ((rc = rms3(w->group_norm))) return rc;
+    if ((rc = launch_linear_lp(ctx, W, a3, 3 * d, w->group_qkv, w->group_qkv_bias, big, 3 * inner, T, 3 * inner, 3 * d,
+                               0, F, JC_F32)))
+        return rc;
+    if ((rc = jc_c2_group_attention(ctx, big, att, live, group_start, group_end, rows, n, heads, dh, inner, JC_F32)))
+        return rc;
+    if ((rc = launch_split_x3(ctx, W, att, inner, a3, T, inner, 0))) return rc;
+    if ((rc = launch_linear_lp(ctx, W, a3, 3 * inner, w->group_o, w->group_o_bias, x, d, T, d, 3 * inner,
+                               JC_GEMM_ACCUMULATE, F, JC_F32)))
+        return rc;
+    // feed-forward sub-layer (Chronos2Forward.java:283-286)
+    if ((rc = rms3(w->mlp_norm))) return rc;
+    if ((rc = launch_linear_lp(ctx, W, a3, 3 * d, w->wi, w->wi_bias, big, dff, T, dff, 3 * d, JC_GEMM_RELU, F, JC_F32)))
+        return rc;
+    if ((rc = launch_split_x3(ctx, W, big, dff, a3, T, dff, 0))) return rc;
+    return launch_linear_lp(ctx, W, a3, 3 * dff, w->wo, w->wo_bias, x, d, T, d, 3 * dff, JC_GEMM_ACCUMULATE, F, JC_F32);
 }
 
 // ---- The rest of the Chronos-2 forward ------------------------------------------------------

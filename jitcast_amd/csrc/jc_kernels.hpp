@@ -81,6 +81,11 @@ hipError_t rms_norm_lp_launch(const float* x, void* y, const float* w, int rows,
                               hipStream_t stream);
 // y[i] = x[i] rounded to the storage type, saturated to its finite range
 hipError_t to_lp_launch(const float* x, void* y, uint64_t count, bool fp16, hipStream_t stream);
+// the three-term fp16 split of x [rows, ldx] fp32 into y [rows, 3k] fp16: [hi | hi | lo] (A operand)
+// or, with weights, [hi | lo | hi] (W operand); k and ldx multiples of 4, x 16-byte aligned
+hipError_t split_x3_launch(const float* x, int ldx, void* y, int rows, int k, bool weights, hipStream_t stream);
+// rms_norm_f32's output as the A-operand split [rows, 3d] fp16
+hipError_t rms_norm_x3_launch(const float* x, void* y, const float* w, int rows, int d, float eps, hipStream_t stream);
 
 // Chronos-2 token moves (d a multiple of 4, 16-byte aligned): the encoder input from the patch
 // embeddings and [REG] (reg may be null when nreg = 0), and the future tokens of the encoder output

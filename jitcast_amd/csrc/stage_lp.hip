@@ -400,6 +400,64 @@ __global__ __launch_bounds__(256) void to_lp(const float* __restrict__ x, T* __r
         y[i] = saturate<T>(x[i]);
 }
 
+// The three-term fp16 split (dtype JC_F16X3). hi = fp16(v), saturated to +-65504 as the FP16
+// twins, and lo = fp16(v - hi). A row of k values becomes 3k fp16 values, [hi | hi | lo] for a
+// GEMM's A operand or [hi | lo | hi] for its W operand, so one fp16 GEMM over K = 3k with fp32
+// accumulation sums a_hi w_hi + a_hi w_lo + a_lo w_hi (fp16 products are exact in fp32).
+// hi + lo = v within 2^-22 |v| + 2^-25 (lo's rounding; below 2^-14 its subnormal spacing 2^-24
+// sets the absolute term), so with the dropped a_lo w_lo each product is within about
+// 2^-20 |a w| + 2^-25 (|a| + |w|), against 2^-11 |a w| for a single fp16 product. Values beyond
+// +-65504 saturate, as in the FP16 GEMM mode.
+__device__ __forceinline__ void split_f16x4(floatx4 v, halfx4& hi, halfx4& lo) {
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        hi[u] = saturate<_Float16>(v[u]);
+        lo[u] = saturate<_Float16>(v[u] - (float)hi[u]);
+    }
+}
+
+// x [rows, ldx] fp32 (k a multiple of 4, ldx of 4, 16-byte aligned) -> y [rows, 3k] fp16
+__global__ __launch_bounds__(256) void split_x3(const float* __restrict__ x, int ldx, _Float16* __restrict__ y,
+                                                int rows, int k, int weights) {
+    const int q = k / 4;
+    const uint64_t total = (uint64_t)rows * q;
+    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+        const int r = (int)(i / q), c = (int)(i % q) * 4;
+        halfx4 hi, lo;
+        split_f16x4(*reinterpret_cast<const floatx4*>(x + (size_t)r * ldx + c), hi, lo);
+        _Float16* yr = y + (size_t)r * 3 * k;
+        *reinterpret_cast<halfx4*>(yr + c) = hi;
+        *reinterpret_cast<halfx4*>(yr + k + c) = weights ? lo : hi;
+        *reinterpret_cast<halfx4*>(yr + 2 * k + c) = weights ? hi : lo;
+    }
+}
+
+// rms_norm_f32's y, written as the A-operand split [hi | hi | lo] of 3d fp16 per row
+__global__ __launch_bounds__(256) void rms_norm_x3(const float* __restrict__ x, _Float16* __restrict__ y,
+                                                   const float* __restrict__ w, int rows, int d, float eps) {
+    const int row = blockIdx.x * 4 + threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    if (row >= rows) return;
+    const floatx4* xr = reinterpret_cast<const floatx4*>(x + (size_t)row * d);
+    float ss = 0.f;
+    for (int i = lane; i < d / 4; i += kWave) {
+        const floatx4 v = xr[i];
+        ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+    const float inv = 1.f / sqrtf(ss / d + eps);
+    const floatx4* wr = reinterpret_cast<const floatx4*>(w);
+    _Float16* yr = y + (size_t)row * 3 * d;
+    for (int i = lane; i < d / 4; i += kWave) {
+        halfx4 hi, lo;
+        split_f16x4(xr[i] * inv * (w ? wr[i] : floatx4{1.f, 1.f, 1.f, 1.f}), hi, lo);
+        *reinterpret_cast<halfx4*>(yr + 4 * i) = hi;
+        *reinterpret_cast<halfx4*>(yr + d + 4 * i) = hi;
+        *reinterpret_cast<halfx4*>(yr + 2 * d + 4 * i) = lo;
+    }
+}
+
 }  // namespace
 
 hipError_t gemm_lp_launch(const GemmLpArgs& g, bool fp16, bool out_lp, int cus, hipStream_t stream) {
@@ -425,6 +483,19 @@ hipError_t rms_norm_lp_launch(const float* x, void* y, const float* w, int rows,
     const dim3 grid((uint32_t)((rows + 3) / 4));
     if (fp16) hipLaunchKernelGGL(rms_norm_lp<_Float16>, grid, dim3(256), 0, stream, x, (_Float16*)y, w, rows, d, eps);
     else hipLaunchKernelGGL(rms_norm_lp<__bf16>, grid, dim3(256), 0, stream, x, (__bf16*)y, w, rows, d, eps);
+    return hipGetLastError();
+}
+
+hipError_t split_x3_launch(const float* x, int ldx, void* y, int rows, int k, bool weights, hipStream_t stream) {
+    const uint64_t blocks = (uint64_t)rows * (k / 4) / 256 + 1;
+    const dim3 grid((uint32_t)(blocks < 8192 ? blocks : 8192));
+    hipLaunchKernelGGL(split_x3, grid, dim3(256), 0, stream, x, ldx, (_Float16*)y, rows, k, weights ? 1 : 0);
+    return hipGetLastError();
+}
+
+hipError_t rms_norm_x3_launch(const float* x, void* y, const float* w, int rows, int d, float eps, hipStream_t stream) {
+    hipLaunchKernelGGL(rms_norm_x3, dim3((uint32_t)((rows + 3) / 4)), dim3(256), 0, stream, x, (_Float16*)y, w, rows, d,
+                       eps);
     return hipGetLastError();
 }
 

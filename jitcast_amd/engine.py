@@ -49,9 +49,9 @@ class HipChronos2Engine(ForecastEngine):
     def __init__(self, config, weights: dict, dtype: str | None = None, device: int | None = None,
                  max_plans: int | None = None, plan_bytes: int | None = None, pipeline_options=None,
                  batch_size: int | None = None, max_tokens: int | None = None):
-        dtype = dtype if dtype is not None else opts.choice("chronos2.hip.dtype", "f32", "f32", "bf16", "fp16")
-        if dtype not in ("f32", "bf16", "fp16"):
-            raise ValueError(f"dtype must be f32, bf16 or fp16, got {dtype}")
+        dtype = dtype if dtype is not None else opts.choice("chronos2.hip.dtype", "f32", "f32", "bf16", "fp16", "f16x3")
+        if dtype not in ("f32", "bf16", "fp16", "f16x3"):
+            raise ValueError(f"dtype must be f32, bf16, fp16 or f16x3, got {dtype}")
         device = device if device is not None else opts.integer("jitcast.hip.device", 0, 0)
         max_plans = max_plans if max_plans is not None else opts.integer("chronos2.hip.plans", 8, 0)
         if plan_bytes is None and max_plans > 0:

@@ -7,7 +7,8 @@ expected; unknown properties are ignored, as the JVM ignores them.
 
 Properties read by this package:
   chronos2.maxTokens        tokens per forward pass before the pipeline splits it (131072)
-  chronos2.hip.dtype        f32 | bf16 | fp16: the encoder's GEMM and time-attention type (f32)
+  chronos2.hip.dtype        f32 | bf16 | fp16 | f16x3: the encoder's GEMM and time-attention type;
+                            f16x3 keeps fp32 results with the GEMMs on three-term fp16 splits (f32)
   chronos2.hip.plans        plans cached per engine, one hipGraph per batch shape; 0 runs eagerly (8)
   chronos2.hip.planBytes    device bytes the cached plans may hold (the device's memory)
   timestral.hip.buckets     pad blocks to shared shapes before the forward (true)

@@ -39,7 +39,7 @@ def _oracle_forward(oracle, c, w):
     return fwd
 
 
-@pytest.mark.parametrize("dt,call_bar,bar", [("f32", 1e-4, 1e-3), ("bf16", 2e-2, 5e-2)])
+@pytest.mark.parametrize("dt,call_bar,bar", [("f32", 1e-4, 1e-3), ("f16x3", 1e-4, 1e-3), ("bf16", 2e-2, 5e-2)])
 def test_engine_mixed_batch_matches_oracle_pipeline(gpu, oracle, checkpoint, dt, call_bar, bar):
     print(f"case engine mixed batch {dt}", flush=True)
     horizon = 100

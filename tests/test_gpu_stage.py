@@ -88,7 +88,13 @@ def _run_layer(x, w, live, group, rows, n, heads, dh, dff, eps, dtype=None):
     xt = _t(x)
     wt = {k: _t(v) for k, v in w.items()}
     code = _lib.JC_F32
-    if dtype is not None:  # the weight matrices in the storage type, converted on the device
+    if dtype == "f16x3":  # the weight matrices as fp16 W-operand splits [n, 3k], made on the device
+        code = _lib.JC_F16X3
+        for k in MATRICES:
+            x3 = torch.empty(wt[k].shape[0], 3 * wt[k].shape[1], dtype=torch.float16, device=DEV)
+            chronos2.split_f16x3(wt[k], x3, weights=True)
+            wt[k] = x3
+    elif dtype is not None:  # the weight matrices in the storage type, converted on the device
         code = {torch.bfloat16: _lib.JC_BF16, torch.float16: _lib.JC_F16}[dtype]
         for k in MATRICES:
             lp = torch.empty(wt[k].shape, dtype=dtype, device=DEV)
@@ -122,6 +128,64 @@ def test_layer_matches_oracle(gpu, oracle, gemm_path, rows, n, heads, dh, d, dff
     print(f"  rel err {err:.3e}", flush=True)
     assert np.isfinite(got).all()
     assert err <= TOL
+
+
+@pytest.mark.parametrize("rows,n,heads,dh,d,dff,bias", [
+    (6, 37, 4, 16, 64, 128, True),
+    (4, 37, 8, 64, 512, 2048, False),    # config 0's layer shape
+    (3, 130, 12, 64, 768, 3072, False),  # config 4's layer shape
+])
+def test_layer_f16x3_matches_oracle(gpu, oracle, gemm_path, rows, n, heads, dh, d, dff, bias):
+    """JC_F16X3: every GEMM on three-term fp16 splits of its operands, fp32 accumulation and outputs,
+    held to the fp32 bar (1e-4), at the configs' initialisation (weights N(0, 0.02))."""
+    print(f"case f16x3 rows={rows} n={n} heads={heads} dh={dh} d={d} dff={dff} bias={bias}", flush=True)
+    w = _layer_weights(41 + d, d, heads * dh, dff, bias)
+    r = np.random.default_rng(45)
+    for k in MATRICES:
+        w[k] = (0.02 * r.standard_normal(w[k].shape)).astype(np.float32)
+    x = np.random.default_rng(42).standard_normal((rows * n, d)).astype(np.float32)
+    live = cases.left_pad_live(43, rows, n, n // 3)
+    group = np.sort(np.random.default_rng(44).integers(0, max(1, rows // 2), rows)).astype(np.int32)
+    got = _run_layer(x, w, live, group, rows, n, heads, dh, dff, 1e-6, "f16x3")
+    exp = oracle.c2_layer(x, w, live, group, rows, n, heads, dh, 1e-6)
+    err = oracle.rel_max_error(got, exp)
+    print(f"  rel err {err:.3e}", flush=True)
+    assert np.isfinite(got).all()
+    assert err <= TOL
+
+
+def _split_reference(v, weights):
+    """numpy's round-to-nearest-even float16 of the saturated value, and of what it leaves."""
+    v = v.astype(np.float32)
+    sat = np.where(np.isnan(v), v, np.clip(v, -65504, 65504)).astype(np.float32)
+    hi = sat.astype(np.float16)
+    rest = (v - hi.astype(np.float32)).astype(np.float32)
+    lo = np.where(np.isnan(rest), rest, np.clip(rest, -65504, 65504)).astype(np.float16)
+    return np.concatenate([hi, lo, hi] if weights else [hi, hi, lo], axis=1)
+
+
+@pytest.mark.parametrize("weights", [False, True])
+def test_split_f16x3_is_exact(gpu, weights):
+    """jc_split_f16x3 bit for bit against numpy's float16 rounding, with a row stride past k, values
+    at fp16's range and past it (saturated), subnormal residues and NaN. hi + lo restores v to 2^-22
+    of v plus half fp16's subnormal spacing (2^-25, where lo is subnormal: |v| below about 0.25)."""
+    rows, k, ld = 37, 68, 72
+    r = np.random.default_rng(9)
+    src = (r.standard_normal((rows, ld)) * np.exp(r.uniform(-12, 8, (rows, ld)))).astype(np.float32)
+    src[0, :6] = [65504.0, -65504.0, 1e6, -3e5, np.nan, 3.0e-8]
+    x = _t(src)
+    y = torch.empty(rows, 3 * k, dtype=torch.float16, device=DEV)
+    chronos2.split_f16x3(x[:, :k], y, weights=weights)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    exp = _split_reference(src[:, :k], weights)
+    np.testing.assert_array_equal(got.view(np.uint16), exp.view(np.uint16))
+    hi = got[:, :k].astype(np.float64)
+    lo = got[:, k:2 * k] if weights else got[:, 2 * k:]
+    v = src[:, :k].astype(np.float64)
+    ok = np.isfinite(v) & (np.abs(v) < 60000)
+    recon = hi + lo.astype(np.float64)
+    assert np.all(np.abs(recon[ok] - v[ok]) <= 2 ** -22 * np.abs(v[ok]) + 2 ** -25)
 
 
 LP = {"bf16": torch.bfloat16, "fp16": torch.float16}
