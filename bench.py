@@ -257,7 +257,7 @@ def layer_line(steps: int, warmup: int, dtype_name: str = "f32") -> dict:
         "workload": f"config 4 encoder-layer shape: 1024 groups x (4 series + 1 known covariate), 133 tokens "
                     f"(128 context patches + REG + 4 future), d_model 768, 12x64, d_ff 3072, {dtype_name}",
         "kernel": "jc_c2_layer (hipBLASLt %s GEMMs)" % {_lib.JC_F32: "fp32", _lib.JC_BF16: "bf16 x bf16 -> fp32 / bf16",
-                                                         _lib.JC_F16X3: "fp16 GEMMs over three-term splits, K = 3k"}[code],
+                                                         _lib.JC_F16X3: "fp16 (three-term splits, K = 3k)"}[code],
         "launch_ms": round(ms, 4),
         "value": round(tf, 2),
         "unit": "TFLOP/s",

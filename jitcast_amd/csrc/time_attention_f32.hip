@@ -30,6 +30,12 @@
 // dims 8c..8c+7 of one key of each 32-key block (8 products and an 8-lane DPP sum give the score),
 // each wave keeps a lazy online softmax over its 8 keys per block and accumulates its share of the
 // output from V^T in LDS, and the four shares are rescaled to a common max once at the end.
+//
+// The last key (Chronos-2, 64-wide heads, rows of 32k + 1 tokens): key n - 1 would be alone in a
+// last 32-key block whose MFMAs and staging cost a full block. It is staged once instead (rotated K
+// and V in LDS), and before the block loop each query takes its score against it on VALU (a 32-dim
+// dot per lane, summed over the lane pair) as the first step of its online softmax: running max
+// = that score, sum = 1, O = V[n - 1]. The folded query adds it in its final combination.
 #include "jc_common.hpp"
 #include "jc_kernels.hpp"
 #include "time_mask.hpp"
@@ -53,6 +59,7 @@ struct F32Lds {
     uint64_t mask[kMaxTokens / kMaskBlock];  // per 64-key word: key validity bits
     int32_t pos[TS ? kMaxTokens : 1];       // table row of every token of the row (Timestral)
     float fold_q[DHP];                       // FOLD: the folded query, rotated and scaled
+    float last_k[DHP], last_v[DHP];          // the last key (rotated, unscaled) and its value
 };
 
 template <int CTRL>
@@ -160,6 +167,9 @@ __global__ __launch_bounds__(kThreads) void time_attention_f32(const TimeArgs a,
     const int bh = logical / a.qgroups;
     const int h = bh % a.heads, r = bh / a.heads;
     const bool fold = FOLD && qg == a.qgroups - 1;  // this workgroup also computes query n - 1
+    // key n - 1 alone in the last block: taken on VALU after the loop
+    constexpr bool kLastOk = !TS && EXACT && DHP == 64 && KB == 32;
+    const bool lastk = kLastOk && a.n > 1 && a.n % KB == 1;
     TimeMask<TS> mask;
     mask.init(a, r);
     const int32_t* vrow = a.valid + (size_t)r * (TS ? a.enc : n);
@@ -228,7 +238,7 @@ __global__ __launch_bounds__(kThreads) void time_attention_f32(const TimeArgs a,
     // 64-key words any query of the workgroup can see (the same in every wave)
     const int qlo = qg * kWaves * kQ, qhi = min(qlo + kWaves * kQ, n) - 1;
     const uint64_t need = __ballot(lane < nwords && mask.any_allowed(lds.mask[lane], lane * kMaskBlock, qlo, qhi));
-    const int nblk = (n + KB - 1) / KB;
+    const int nblk = (n - (lastk ? 1 : 0) + KB - 1) / KB;
     auto next_block = [&](int after) {
         const int b = after + 1;
         const int w = b * KB / kMaskBlock;
@@ -273,12 +283,55 @@ __global__ __launch_bounds__(kThreads) void time_attention_f32(const TimeArgs a,
         stage.load(rk_at(kb), ROPE ? rt_at(kb) : rk_at(kb), lds.pos, kb * KB, n, tid, inner, dh);
         stage.store(lds, 0, tid);
     }
+    if (kLastOk && lastk && wave == 1) {
+        // key n - 1's dims e and e + 32, rotated at its table row as staging rotates every key (loaded
+        // here, after Q's prologue registers are free, beside the first block's staging)
+        const int kl = n - 1;
+        const float* kp = qkv + ((size_t)r * n + kl) * 3 * inner + inner + h * dh;
+        if (lane < DHP / 2) {
+            const int e = lane;
+            float x = kp[e], y = kp[DHP / 2 + e];
+            if (ROPE) {
+                const float c = a.table[(size_t)kl * dh + e], sn = a.table[(size_t)kl * dh + DHP / 2 + e];
+                const float rx = x * c - y * sn, ry = y * c + x * sn;
+                x = rx;
+                y = ry;
+            }
+            lds.last_k[e] = x;
+            lds.last_k[DHP / 2 + e] = y;
+        }
+        lds.last_v[lane] = kp[inner + lane];
+    }
     __syncthreads();
 
     floatx16 o_acc[kTiles];
 #pragma unroll
     for (int t = 0; t < kTiles; t++) o_acc[t] = floatx16{0};
     float m_run = -INFINITY, l_run = 0.f;
+    if (kLastOk && lastk && ((lds.mask[(n - 1) / kMaskBlock] >> ((n - 1) % kMaskBlock)) & 1ull)) {
+        // the live last key opens the online softmax (uniform over the workgroup): m = its score,
+        // P = 1, O = its value. Lane (j, g) holds dims 32g..32g+31 of query j, so the pair sum of
+        // the lane's partial dot is the whole score.
+        const float* kp = &lds.last_k[g * kHalfP];
+        float d = 0.f;
+#pragma unroll
+        for (int s4 = 0; s4 < kSteps / 4; s4++) {
+            const floatx4 kv = *reinterpret_cast<const floatx4*>(kp + 4 * s4);
+#pragma unroll
+            for (int u = 0; u < 4; u++) d += qreg[4 * s4 + u] * kv[u];
+        }
+        m_run = pair_sum(d);
+        l_run = g == 0 ? 1.f : 0.f;  // the pair sum at the end counts it once
+#pragma unroll
+        for (int t = 0; t < kTiles; t++) {
+#pragma unroll
+            for (int a4 = 0; a4 < 4; a4++) {
+                const floatx4 vv = *reinterpret_cast<const floatx4*>(&lds.last_v[32 * t + 8 * a4 + 4 * g]);
+#pragma unroll
+                for (int u = 0; u < 4; u++) o_acc[t][4 * a4 + u] = vv[u];
+            }
+        }
+    }
     // FOLD: this wave's softmax state for the folded query over its keys (8 per block)
     float f_m = -INFINITY, f_l = 0.f;
     floatx4 f_oa = floatx4{0.f, 0.f, 0.f, 0.f}, f_ob = f_oa;
@@ -454,6 +507,15 @@ __global__ __launch_bounds__(kThreads) void time_attention_f32(const TimeArgs a,
                 mw[w] = lds.k[0][w * (DHP + 2) + DHP];
                 mx = fmaxf(mx, mw[w]);
             }
+            // the folded query against the last key, when the loop left it out and it is live
+            float sl = -INFINITY;
+            if (lastk && ((lds.mask[(n - 1) / kMaskBlock] >> ((n - 1) % kMaskBlock)) & 1ull)) {
+                float d = lds.fold_q[lane] * lds.last_k[lane];
+#pragma unroll
+                for (int off = 32; off > 0; off >>= 1) d += __shfl_xor(d, off);
+                sl = d;
+                mx = fmaxf(mx, sl);
+            }
             float o = 0.f, l = 0.f;
             if (mx != -INFINITY) {
 #pragma unroll
@@ -462,6 +524,9 @@ __global__ __launch_bounds__(kThreads) void time_attention_f32(const TimeArgs a,
                     o += f * lds.k[0][w * (DHP + 2) + lane];
                     l += f * lds.k[0][w * (DHP + 2) + DHP + 1];
                 }
+                const float f = fast_exp2(sl - mx);  // 0 without the last key
+                o += f * lds.last_v[lane];
+                l += f;
             }
             float* op = static_cast<float*>(a.out) + ((size_t)r * n + n - 1) * inner + h * dh;
             op[lane] = l > 0.f ? o / l : 0.f;

@@ -219,6 +219,30 @@ def test_fp32_folded_last_query(gpu, oracle, n, kind):
     assert np.isnan(got[:, :, heads * dh:]).all(), "columns past heads * dh are not written"
 
 
+@pytest.mark.parametrize("n", [33, 161, 513])
+@pytest.mark.parametrize("pattern", ["last dead", "only last", "all", "pad"])
+def test_fp32_last_key(gpu, oracle, n, pattern):
+    """Rows of 32k + 1 tokens: key n - 1 is not staged as a block of its own but added on VALU after
+    the block loop (with the folded query too at n = 128k + 1). Checked with that key dead among live
+    ones, as the only live key, and with every key or a left-padded row live."""
+    rows, heads, dh, inner = 3, 2, 64, 136
+    print(f"case last key n={n} {pattern}", flush=True)
+    qkv = cases.qkv(43, rows * n, inner)
+    live = cases.left_pad_live(43, rows, n, n // 2) if pattern == "pad" else np.ones((rows, n), np.int32)
+    if pattern == "last dead":
+        live[:, n - 1] = 0
+    elif pattern == "only last":
+        live[:] = 0
+        live[:, n - 1] = 1
+    got = _run(qkv, live, rows, n, heads, dh, inner)[:, : heads * dh]
+    exp = oracle.c2_time_attention(qkv, live, rows, n, heads, dh, inner)[:, : heads * dh]
+    assert oracle.rel_max_error(got, exp) <= TOL_F32
+    if pattern == "only last":
+        v = qkv.reshape(rows, n, 3 * inner)[:, n - 1, 2 * inner:2 * inner + heads * dh]
+        np.testing.assert_allclose(got.reshape(rows, n, -1), np.broadcast_to(v[:, None], (rows, n, heads * dh)),
+                                   rtol=1e-6, atol=1e-6)
+
+
 @pytest.mark.parametrize("n", [65, 129])
 def test_fp32_without_table_is_plain_attention(gpu, n):
     """rope_table NULL: qkv is taken as already rotated (the reference's separate rope task ran)."""
