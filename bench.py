@@ -251,7 +251,8 @@ def layer_line(steps: int, warmup: int, dtype_name: str = "f32") -> dict:
     # peak with the algorithmic (fp32) flops, and the executed MFMA flops are reported beside them
     peak = PEAK_FP32_TFLOPS if code == _lib.JC_F32 else PEAK_BF16_TFLOPS
     tokens = case.rows * case.n
-    log(f"layer {dtype_name}: {ms:.3f} ms, {tf:.1f} TFLOP/s ({100 * tf / peak:.1f}% of the {dtype_name} MFMA peak), "
+    peak_name = {"f16x3": "fp16 MFMA peak, fp32-equivalent flops"}.get(dtype_name, f"{dtype_name} MFMA peak")
+    log(f"layer {dtype_name}: {ms:.3f} ms, {tf:.1f} TFLOP/s ({100 * tf / peak:.1f}% of the {peak_name}), "
         f"{tokens / (ms * 1e-3) / 1e6:.1f} M tokens/s")
     res = {
         "workload": f"config 4 encoder-layer shape: 1024 groups x (4 series + 1 known covariate), 133 tokens "
