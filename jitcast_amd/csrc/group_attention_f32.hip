@@ -59,8 +59,11 @@ struct Job {
 };
 
 
-template <int DHP, bool TS, bool EXACT>
+// X3 (Chronos-2, 64-wide heads; the JC_F16X3 layer): out holds fp16 rows of 3 * inner values, the
+// O projection's A operand [hi | hi | lo] (the three-term split of each fp32 output value).
+template <int DHP, bool TS, bool EXACT, bool X3>
 __global__ __launch_bounds__(kWave) void group_attention_f32(const GroupArgs a, int dh_rt) {
+    static_assert(!X3 || (!TS && EXACT && DHP == 64), "split output: Chronos-2, 64-wide heads");
     static_assert(DHP % 16 == 0 && DHP <= 128, "head width");
     constexpr int kM = DHP / 16;            // 16-dim groups: K/Q loads per lane, and output dim tiles
     constexpr int kQT = DHP <= 64 ? 4 : 2;  // query tiles held in registers at once
@@ -118,7 +121,12 @@ __global__ __launch_bounds__(kWave) void group_attention_f32(const GroupArgs a, 
 #pragma unroll
                     for (int u = 0; u < 4; u++) v[u] *= 1.f / (1.f + fast_exp2(-gv[u] * kLog2e));
                 }
-                *reinterpret_cast<floatx4*>(a.out + off + e) = v;
+                if constexpr (X3) {
+                    store_split_row(reinterpret_cast<_Float16*>(a.out) + ((size_t)row * tok_n + t) * 3 * inner, inner,
+                                    h * dh + e, v);
+                } else {
+                    *reinterpret_cast<floatx4*>(a.out + off + e) = v;
+                }
             }
         }
         return;
@@ -289,7 +297,13 @@ __global__ __launch_bounds__(kWave) void group_attention_f32(const GroupArgs a, 
 #pragma unroll
                                     for (int u = 0; u < 4; u++) v[u] *= 1.f / (1.f + fast_exp2(-gv[u] * kLog2e));
                                 }
-                                *reinterpret_cast<floatx4*>(a.out + off + 16 * m) = v;
+                                if constexpr (X3) {
+                                    store_split_row(
+                                        reinterpret_cast<_Float16*>(a.out) + ((size_t)qrow * tok_n + t) * 3 * inner,
+                                        inner, cur.h * dh + 4 * g + 16 * m, v);
+                                } else {
+                                    *reinterpret_cast<floatx4*>(a.out + off + 16 * m) = v;
+                                }
                             }
                         }
                     }
@@ -303,11 +317,12 @@ __global__ __launch_bounds__(kWave) void group_attention_f32(const GroupArgs a, 
 
 }  // namespace
 
-template <int DHP, bool TS, bool EXACT>
+template <int DHP, bool TS, bool EXACT, bool X3 = false>
 static hipError_t launch_group(GroupArgs a, int dh, hipStream_t stream) {
     a.rtiles = (a.rows + kRT - 1) / kRT;
     const uint64_t grid = (uint64_t)a.rtiles * a.n;
-    hipLaunchKernelGGL((group_attention_f32<DHP, TS, EXACT>), dim3((uint32_t)grid), dim3(kWave), 0, stream, a, dh);
+    hipLaunchKernelGGL((group_attention_f32<DHP, TS, EXACT, X3>), dim3((uint32_t)grid), dim3(kWave), 0, stream, a,
+                       dh);
     return hipGetLastError();
 }
 
@@ -329,6 +344,11 @@ static hipError_t dispatch_group(const GroupArgs& a, int dh, hipStream_t stream)
 hipError_t group_attention_f32_launch(const GroupArgs& a, int dh, bool ts, hipStream_t stream) {
     if (dh < 8 || dh > 128 || dh % 8) return hipErrorInvalidValue;
     return ts ? dispatch_group<true>(a, dh, stream) : dispatch_group<false>(a, dh, stream);
+}
+
+hipError_t group_attention_f32_x3_launch(const GroupArgs& a, int dh, hipStream_t stream) {
+    if (dh != 64) return hipErrorInvalidValue;
+    return launch_group<64, false, true, true>(a, dh, stream);
 }
 
 }  // namespace jc

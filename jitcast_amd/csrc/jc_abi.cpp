@@ -349,12 +349,11 @@ static int launch_time(jc_ctx* ctx, const char* W, const jc::TimeArgs& a, int dh
     return e == hipSuccess ? JC_OK : hip_fail(W, e);
 }
 
-int jc_c2_time_attention(jc_ctx* ctx, const void* qkv, void* out, const int32_t* live, const float* table, int rows,
-                         int n, int heads, int dh, int inner, int dtype) {
-    const char* W = "jc_c2_time_attention";
-    int rc = use(ctx, W);
-    if (rc) return rc;
-    rc = check_time_common(W, qkv, out, table, nullptr, rows, n, heads, dh, inner, dtype, 64);
+// jc_c2_time_attention after use(). x3 (fp32, dh 64): out is the JC_F16X3 layer's split operand, fp16
+// [rows*n, 3*inner] rows [hi | hi | lo] of each output value.
+static int c2_time(jc_ctx* ctx, const char* W, const void* qkv, void* out, const int32_t* live, const float* table,
+                   int rows, int n, int heads, int dh, int inner, int dtype, bool x3) {
+    int rc = check_time_common(W, qkv, out, table, nullptr, rows, n, heads, dh, inner, dtype, 64);
     if (rc || (size_t)rows * n == 0) return rc;
     if (!live) return fail(JC_EINVAL, "%s: null live mask", W);
     jc::TimeArgs a{};
@@ -370,7 +369,20 @@ int jc_c2_time_attention(jc_ctx* ctx, const void* qkv, void* out, const int32_t*
     a.ll = n;
     a.table_rows = n;
     a.qscale = 1.4426950408889634f;  // unscaled scores, exp via exp2
+    if (x3) {
+        if (dtype != JC_F32) return fail(JC_EINVAL, "%s: the split output needs fp32", W);
+        hipError_t e = jc::time_attention_f32_x3_launch(a, dh, ctx->stream);
+        return e == hipSuccess ? JC_OK : hip_fail(W, e);
+    }
     return launch_time(ctx, W, a, dh, false, dtype);
+}
+
+int jc_c2_time_attention(jc_ctx* ctx, const void* qkv, void* out, const int32_t* live, const float* table, int rows,
+                         int n, int heads, int dh, int inner, int dtype) {
+    const char* W = "jc_c2_time_attention";
+    int rc = use(ctx, W);
+    if (rc) return rc;
+    return c2_time(ctx, W, qkv, out, live, table, rows, n, heads, dh, inner, dtype, false);
 }
 
 int jc_ts_rope_table(int enc, int n, int dh, int rope_dim, float theta, float* table) {
@@ -457,12 +469,11 @@ static int check_group_common(const char* W, const void* qkv, const void* out, c
     return JC_OK;
 }
 
-int jc_c2_group_attention(jc_ctx* ctx, const void* qkv, void* out, const int32_t* live, const int32_t* group_start,
-                          const int32_t* group_end, int rows, int n, int heads, int dh, int inner, int dtype) {
-    const char* W = "jc_c2_group_attention";
-    int rc = use(ctx, W);
-    if (rc) return rc;
-    rc = check_group_common(W, qkv, out, nullptr, group_start, group_end, rows, n, heads, dh, inner, dtype, 64);
+// jc_c2_group_attention after use(); x3 as for c2_time.
+static int c2_group(jc_ctx* ctx, const char* W, const void* qkv, void* out, const int32_t* live,
+                    const int32_t* group_start, const int32_t* group_end, int rows, int n, int heads, int dh, int inner,
+                    int dtype, bool x3) {
+    int rc = check_group_common(W, qkv, out, nullptr, group_start, group_end, rows, n, heads, dh, inner, dtype, 64);
     if (rc || (size_t)rows * n == 0) return rc;
     if (!live) return fail(JC_EINVAL, "%s: null live mask", W);
     jc::GroupArgs a{};
@@ -477,8 +488,17 @@ int jc_c2_group_attention(jc_ctx* ctx, const void* qkv, void* out, const int32_t
     a.inner = inner;
     a.enc = n;
     a.qscale = 1.4426950408889634f;  // unscaled scores, exp via exp2
-    hipError_t e = jc::group_attention_f32_launch(a, dh, false, ctx->stream);
+    hipError_t e = x3 ? jc::group_attention_f32_x3_launch(a, dh, ctx->stream)
+                      : jc::group_attention_f32_launch(a, dh, false, ctx->stream);
     return e == hipSuccess ? JC_OK : hip_fail(W, e);
+}
+
+int jc_c2_group_attention(jc_ctx* ctx, const void* qkv, void* out, const int32_t* live, const int32_t* group_start,
+                          const int32_t* group_end, int rows, int n, int heads, int dh, int inner, int dtype) {
+    const char* W = "jc_c2_group_attention";
+    int rc = use(ctx, W);
+    if (rc) return rc;
+    return c2_group(ctx, W, qkv, out, live, group_start, group_end, rows, n, heads, dh, inner, dtype, false);
 }
 
 int jc_ts_variate_attention(jc_ctx* ctx, const void* qkv, void* out, const int32_t* key_valid,
@@ -937,8 +957,9 @@ int jc_split_f16x3(jc_ctx* ctx, const float* src, int ld_src, void* dst, int row
 }
 
 // The JC_F32 layer with every GEMM on the operands' three-term fp16 splits: the norms write the
-// A-operand split of hn directly, the attention outputs and the MLP activation are split before their
-// GEMMs, and every GEMM (K = 3k, fp32 accumulation) writes fp32.
+// A-operand split of hn directly, the attention kernels write the split of their outputs (64-wide
+// heads; other widths go through fp32 and a split pass), the MLP activation is split before its
+// GEMM, and every GEMM (K = 3k, fp32 accumulation) writes fp32.
 static int layer_x3(jc_ctx* ctx, const char* W, float* x, const jc_c2_layer_weights* w, const int32_t* live,
                     const float* table, const int32_t* group_start, const int32_t* group_end, void* workspace, int rows,
                     int n, int d, int heads, int dh, int dff, float eps) {
@@ -960,8 +981,13 @@ static int layer_x3(jc_ctx* ctx, const char* W, float* x, const jc_c2_layer_weig
     if ((rc = launch_linear_lp(ctx, W, a3, 3 * d, w->time_qkv, w->time_qkv_bias, big, 3 * inner, T, 3 * inner, 3 * d, 0,
                                F, JC_F32)))
         return rc;
-    if ((rc = jc_c2_time_attention(ctx, big, att, live, table, rows, n, heads, dh, inner, JC_F32))) return rc;
-    if ((rc = launch_split_x3(ctx, W, att, inner, a3, T, inner, 0))) return rc;
+    const bool fused = dh == 64;  // the attention kernels write the split themselves
+    if (fused) {
+        if ((rc = c2_time(ctx, W, big, a3, live, table, rows, n, heads, dh, inner, JC_F32, true))) return rc;
+    } else {
+        if ((rc = c2_time(ctx, W, big, att, live, table, rows, n, heads, dh, inner, JC_F32, false))) return rc;
+        if ((rc = launch_split_x3(ctx, W, att, inner, a3, T, inner, 0))) return rc;
+    }
     if ((rc = launch_linear_lp(ctx, W, a3, 3 * inner, w->time_o, w->time_o_bias, x, d, T, d, 3 * inner,
                                JC_GEMM_ACCUMULATE, F, JC_F32)))
         return rc;
@@ -970,9 +996,14 @@ static int layer_x3(jc_ctx* ctx, const char* W, float* x, const jc_c2_layer_weig
     if ((rc = launch_linear_lp(ctx, W, a3, 3 * d, w->group_qkv, w->group_qkv_bias, big, 3 * inner, T, 3 * inner, 3 * d,
                                0, F, JC_F32)))
         return rc;
-    if ((rc = jc_c2_group_attention(ctx, big, att, live, group_start, group_end, rows, n, heads, dh, inner, JC_F32)))
-        return rc;
-    if ((rc = launch_split_x3(ctx, W, att, inner, a3, T, inner, 0))) return rc;
+    if (fused) {
+        if ((rc = c2_group(ctx, W, big, a3, live, group_start, group_end, rows, n, heads, dh, inner, JC_F32, true)))
+            return rc;
+    } else {
+        if ((rc = c2_group(ctx, W, big, att, live, group_start, group_end, rows, n, heads, dh, inner, JC_F32, false)))
+            return rc;
+        if ((rc = launch_split_x3(ctx, W, att, inner, a3, T, inner, 0))) return rc;
+    }
     if ((rc = launch_linear_lp(ctx, W, a3, 3 * inner, w->group_o, w->group_o_bias, x, d, T, d, 3 * inner,
                                JC_GEMM_ACCUMULATE, F, JC_F32)))
         return rc;

@@ -12,6 +12,9 @@ namespace jc {
 // Chronos-2 (ts = false) or Timestral (ts = true) time attention (time_mask.hpp); a.qgroups is set
 // by the launcher. fp32: dh a multiple of 8, at most 128; bf16/fp16: a multiple of 16, at most 128.
 hipError_t time_attention_f32_launch(const TimeArgs& a, int dh, bool ts, hipStream_t stream);
+// Chronos-2 with 64-wide heads only (else hipErrorInvalidValue): out is fp16 [rows*n, 3*inner], each
+// output value's three-term split [hi | hi | lo] (the JC_F16X3 layer's A operand of the O projection).
+hipError_t time_attention_f32_x3_launch(const TimeArgs& a, int dh, hipStream_t stream);
 hipError_t time_attention_lp_launch(const TimeArgs& a, int dh, bool ts, bool fp16, hipStream_t stream);
 int time_attention_max_tokens();
 // The row-wide bf16/fp16 kernel: 8-wave workgroups of 256 queries of one (row, head); dh 32 or 64;
@@ -43,6 +46,9 @@ struct GroupArgs {
 // Chronos-2 group attention (ts = false) or Timestral variate attention (ts = true); a.rtiles is
 // set by the launcher. dh a multiple of 8, at most 128 (64 for Chronos-2).
 hipError_t group_attention_f32_launch(const GroupArgs& a, int dh, bool ts, hipStream_t stream);
+// Chronos-2 with 64-wide heads only (else hipErrorInvalidValue): a.out is read as fp16 [rows*n, 3*inner],
+// each output value's three-term split [hi | hi | lo].
+hipError_t group_attention_f32_x3_launch(const GroupArgs& a, int dh, hipStream_t stream);
 
 hipError_t fill_normal_launch(float* out, uint64_t count, uint64_t stream_seed, double mean, double stdv,
                               hipStream_t stream);

@@ -12,7 +12,6 @@ namespace lp {
 constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer, 32-bit data format (gfx9 family)
 
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-typedef _Float16 halfx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 

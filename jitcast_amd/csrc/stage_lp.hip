@@ -407,14 +407,7 @@ __global__ __launch_bounds__(256) void to_lp(const float* __restrict__ x, T* __r
 // hi + lo = v within 2^-22 |v| + 2^-25 (lo's rounding; below 2^-14 its subnormal spacing 2^-24
 // sets the absolute term), so with the dropped a_lo w_lo each product is within about
 // 2^-20 |a w| + 2^-25 (|a| + |w|), against 2^-11 |a w| for a single fp16 product. Values beyond
-// +-65504 saturate, as in the FP16 GEMM mode.
-__device__ __forceinline__ void split_f16x4(floatx4 v, halfx4& hi, halfx4& lo) {
-#pragma unroll
-    for (int u = 0; u < 4; u++) {
-        hi[u] = saturate<_Float16>(v[u]);
-        lo[u] = saturate<_Float16>(v[u] - (float)hi[u]);
-    }
-}
+// +-65504 saturate, as in the FP16 GEMM mode. split_f16x4 (jc_common.hpp) makes the pieces.
 
 // x [rows, ldx] fp32 (k a multiple of 4, ldx of 4, 16-byte aligned) -> y [rows, 3k] fp16
 __global__ __launch_bounds__(256) void split_x3(const float* __restrict__ x, int ldx, _Float16* __restrict__ y,

@@ -36,6 +36,10 @@
 // and V in LDS), and before the block loop each query takes its score against it on VALU (a 32-dim
 // dot per lane, summed over the lane pair) as the first step of its online softmax: running max
 // = that score, sum = 1, O = V[n - 1]. The folded query adds it in its final combination.
+//
+// X3 (Chronos-2, 64-wide heads; the JC_F16X3 layer): out is the O projection's A operand, fp16
+// rows of 3 * inner values [hi | hi | lo] (the three-term split of each fp32 output value), so the
+// layer needs no separate split pass over the attention output.
 #include "jc_common.hpp"
 #include "jc_kernels.hpp"
 #include "time_mask.hpp"
@@ -143,9 +147,10 @@ struct KvStage {
 };
 
 // EXACT: the head is exactly DHP wide, so every head-width expression folds to a constant
-template <int DHP, int KB, bool ROPE, bool TS, bool EXACT, bool FOLD>
+template <int DHP, int KB, bool ROPE, bool TS, bool EXACT, bool FOLD, bool X3>
 __global__ __launch_bounds__(kThreads) void time_attention_f32(const TimeArgs a, int dh_rt) {
     const int dh = EXACT ? DHP : dh_rt;
+    static_assert(!X3 || (!TS && EXACT && DHP == 64), "split output: Chronos-2, 64-wide heads");
     static_assert(DHP % 16 == 0 && DHP <= 128, "head width");
     static_assert(!FOLD || (!TS && EXACT && DHP == 64 && KB == 32), "the folded query: Chronos-2, 64-wide heads");
     static_assert(KB == 32 || KB == 64, "key block");
@@ -528,13 +533,44 @@ __global__ __launch_bounds__(kThreads) void time_attention_f32(const TimeArgs a,
                 o += f * lds.last_v[lane];
                 l += f;
             }
-            float* op = static_cast<float*>(a.out) + ((size_t)r * n + n - 1) * inner + h * dh;
-            op[lane] = l > 0.f ? o / l : 0.f;
+            const float res = l > 0.f ? o / l : 0.f;
+            if constexpr (X3) {
+                store_split_one(static_cast<_Float16*>(a.out) + ((size_t)r * n + n - 1) * 3 * inner, inner,
+                                h * dh + lane, res);
+            } else {
+                float* op = static_cast<float*>(a.out) + ((size_t)r * n + n - 1) * inner + h * dh;
+                op[lane] = res;
+            }
         }
     }
 
     // every lane reaches the swap (its partner holds the other half of the same query)
     const float l = pair_sum(l_run);
+    if constexpr (X3) {
+        // Lanes (j, 0) and (j, 1) trade halves of each 16-dim run (v_permlane32_swap), so each holds 8
+        // consecutive dims: 32t + 16p + 8g + (0..7), from O^T regs 8p + u (dims 32t + 16p + 4g + u) and
+        // 8p + 4 + u (dims 32t + 16p + 8 + 4g + u). Each piece of the split then goes out as one
+        // 16-byte store.
+        const float inv = l > 0.f ? 1.f / l : 0.f;
+        _Float16* orow = static_cast<_Float16*>(a.out) + ((size_t)r * n + q0 + j) * 3 * inner + h * dh;
+#pragma unroll
+        for (int t = 0; t < kTiles; t++) {
+#pragma unroll
+            for (int p = 0; p < 2; p++) {
+                floatx4 d0, d4;
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(o_acc[t][8 * p + u] * inv),
+                                                                     __float_as_uint(o_acc[t][8 * p + 4 + u] * inv),
+                                                                     false, false);
+                    d0[u] = __uint_as_float(sw[0]);
+                    d4[u] = __uint_as_float(sw[1]);
+                }
+                if (j < nq) store_split_row8(orow, inner, 32 * t + 16 * p + 8 * g, d0, d4);
+            }
+        }
+        return;
+    }
     if (j < nq) {
         const float inv = l > 0.f ? 1.f / l : 0.f;
         const size_t tok = (size_t)r * n + q0 + j;
@@ -565,18 +601,18 @@ __global__ __launch_bounds__(kThreads) void time_attention_f32(const TimeArgs a,
 
 }  // namespace
 
-template <int DHP, int KB, bool TS, bool EXACT, bool FOLD>
+template <int DHP, int KB, bool TS, bool EXACT, bool FOLD, bool X3>
 static void launch_f32_rope(const TimeArgs& a, int dh, uint64_t grid, hipStream_t stream) {
     if (a.table) {
-        hipLaunchKernelGGL((time_attention_f32<DHP, KB, true, TS, EXACT, FOLD>), dim3((uint32_t)grid), dim3(kThreads), 0,
-                           stream, a, dh);
+        hipLaunchKernelGGL((time_attention_f32<DHP, KB, true, TS, EXACT, FOLD, X3>), dim3((uint32_t)grid),
+                           dim3(kThreads), 0, stream, a, dh);
     } else {
-        hipLaunchKernelGGL((time_attention_f32<DHP, KB, false, TS, EXACT, FOLD>), dim3((uint32_t)grid), dim3(kThreads),
-                           0, stream, a, dh);
+        hipLaunchKernelGGL((time_attention_f32<DHP, KB, false, TS, EXACT, FOLD, X3>), dim3((uint32_t)grid),
+                           dim3(kThreads), 0, stream, a, dh);
     }
 }
 
-template <int DHP, bool TS, bool EXACT>
+template <int DHP, bool TS, bool EXACT, bool X3 = false>
 static hipError_t launch_f32(TimeArgs a, int dh, hipStream_t stream) {
     constexpr int KB = 32;  // 32-key blocks (64 measured slower on config 1)
     const int tiles = (a.n + kQ - 1) / kQ;
@@ -587,11 +623,11 @@ static hipError_t launch_f32(TimeArgs a, int dh, hipStream_t stream) {
     const uint64_t grid = (uint64_t)a.rows * a.heads * a.qgroups;
     if constexpr (kCanFold) {
         if (fold) {
-            launch_f32_rope<DHP, KB, TS, EXACT, true>(a, dh, grid, stream);
+            launch_f32_rope<DHP, KB, TS, EXACT, true, X3>(a, dh, grid, stream);
             return hipGetLastError();
         }
     }
-    launch_f32_rope<DHP, KB, TS, EXACT, false>(a, dh, grid, stream);
+    launch_f32_rope<DHP, KB, TS, EXACT, false, X3>(a, dh, grid, stream);
     return hipGetLastError();
 }
 
@@ -612,6 +648,11 @@ static hipError_t dispatch_f32(const TimeArgs& a, int dh, hipStream_t stream) {
 hipError_t time_attention_f32_launch(const TimeArgs& a, int dh, bool ts, hipStream_t stream) {
     if (dh < 8 || dh > 128 || dh % 8) return hipErrorInvalidValue;
     return ts ? dispatch_f32<true>(a, dh, stream) : dispatch_f32<false>(a, dh, stream);
+}
+
+hipError_t time_attention_f32_x3_launch(const TimeArgs& a, int dh, hipStream_t stream) {
+    if (dh != 64) return hipErrorInvalidValue;
+    return launch_f32<64, false, true, true>(a, dh, stream);
 }
 
 int time_attention_max_tokens() { return kMaxTokens; }
