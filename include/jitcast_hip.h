@@ -344,10 +344,11 @@ int64_t jc_c2_layer_workspace_bytes(int rows, int n, int d, int inner, int dff, 
  * accumulation (the reference's FP16 GEMM modes, Chronos2Forward.java:377-409, GemmMode.HALF), the
  * time attention runs in the storage type, the group attention in fp32, and x (the residual
  * stream), the norms and the accumulations stay fp32. JC_F16X3 (no reference counterpart): every
- * GEMM runs on its operands' three-term fp16 splits (jc_split_f16x3; the norms write the split
- * directly), with fp32 accumulation and fp32 outputs; the attention, the norms and x are fp32, as in
- * JC_F32, whose accuracy it keeps to about 2^-20 per product (plus 2^-25 times the other operand
- * where lo is subnormal, for operands below about 2^-2).
+ * GEMM runs on its operands' three-term fp16 splits (jc_split_f16x3; the norms, and the attention
+ * kernels for 64-wide heads, write the split directly), with fp32 accumulation and fp32 outputs;
+ * the attention, the norms and x are fp32, as in JC_F32, whose accuracy it keeps to about 2^-20 per
+ * product (plus 2^-25 times the other operand where lo is subnormal, for operands below about
+ * 2^-2).
  */
 int jc_c2_layer(jc_ctx *ctx, float *x, const jc_c2_layer_weights *w, const int32_t *live, const float *table,
                 const int32_t *group_start, const int32_t *group_end, void *workspace, int rows, int n, int d,
