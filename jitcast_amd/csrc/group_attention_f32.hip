@@ -137,8 +137,10 @@ __global__ __launch_bounds__(kWave) void group_attention_f32(const GroupArgs a, 
         jb.valid = rest != 0;
         int b = jb.valid ? __builtin_ctz(rest) : 0;
         jb.gs = r0 + b;
-        // clamped into [gs+1, rows]: a group always holds its first row and only rows that exist
-        jb.ge = jb.valid ? min(max(a.gend[jb.gs], jb.gs + 1), rows) : jb.gs + 1;
+        // clamped into [gs+1, rows]: a group always holds its first row and only rows that exist.
+        // Its end comes from the prologue's load (lane b holds gend[r0 + b]; b is wave-uniform), not
+        // from memory: a load here would stall every group change on its latency.
+        jb.ge = jb.valid ? min(max(__builtin_amdgcn_readlane(ge_l, b), jb.gs + 1), rows) : jb.gs + 1;
         jb.qc = 0;
         jb.h = 0;
         jb.kt = 0;
