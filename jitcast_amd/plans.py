@@ -19,12 +19,17 @@ from .runtime import context
 
 
 class Plan:
-    """A captured, instantiated hipGraph (jc_plan)."""
+    """A captured, instantiated hipGraph (jc_plan) of one device."""
 
-    def __init__(self, handle: ctypes.c_void_p):
+    def __init__(self, handle: ctypes.c_void_p, device: int = 0):
         self.handle = handle
+        self.device = device
 
     def launch(self) -> None:
+        """Replays the graph on torch's current stream: jc_plan_launch launches on the stream its
+        context is bound to, so the context is bound to the current stream first (the last binding
+        may have been to another stream, such as the one a capture ran on)."""
+        context(self.device)
         _lib.call("jc_plan_launch", self.handle)
 
     def adopt(self, dptr: int, nbytes: int) -> None:
@@ -62,7 +67,7 @@ def capture(shape_key: int, device: int = 0):
     finally:
         h = ctypes.c_void_p()
         _lib.call("jc_plan_end", ctx.handle, ctypes.byref(h))
-        box.append(Plan(h))
+        box.append(Plan(h, device))
 
 
 K = TypeVar("K", bound=Hashable)
