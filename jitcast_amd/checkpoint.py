@@ -13,6 +13,14 @@ reads them, and written for the benchmark's random-init configurations.
                       attention sublayer, Chronos2Weights.qkv)
   write_safetensors, write_chronos2
                       the inverse, for synthetic checkpoints
+  parse_ts_config     TimestralConfig.fromJson (J/timestral/TimestralConfig.java:162-240): only known
+                      keys, no biases in attention or MLP, no global stabilisation, the block schedule,
+                      increasing quantile knots holding 0.5, the attention gates
+  load_timestral      TimestralWeights.load (J/timestral/TimestralWeights.java:83-120): every tensor
+                      bound once by name and exact F32 shape; the weights come back in
+                      HipTimestralModel's layout (q|k|v rows heads-major, TimestralWeights.qkv; the
+                      MLP up projection with its SiLU half first, TimestralWeights.mlpUp)
+  write_timestral     the inverse, for synthetic checkpoints
 
 Errors are ValueError (the reference's IllegalArgumentException) or OSError.
 """
@@ -334,4 +342,188 @@ def write_chronos2(checkpoint_dir, c, weights: dict) -> Path:
         else:
             tensors[name] = weights[key]
     write_safetensors(d / "model.safetensors", tensors, {"format": "pt"})
+    return d
+
+
+# ---- Timestral ---------------------------------------------------------------------------------
+
+_TS_KEYS = {"patch_size", "d_model", "num_heads", "mlp_hidden_dim", "block_schedule", "quantile_knots", "block_size",
+            "context_length", "rope_theta", "rope_partial_factor", "norm_eps", "attn_bias", "mlp_bias", "time_attn_gate",
+            "variate_attn_gate", "minimum_scale", "use_asinh", "stabilize_with_global", "covariate_enabled",
+            "split_context_horizon_attn", "attend_missing_patches", "quantile_width_factor"}
+_TS_KINDS = {"time": (True,), "variate": (False,), "time_variate": (True, False), "variate_time": (False, True)}
+
+
+def _ts_gate(m: dict, key: str) -> bool:
+    g = _str(m, key, "sdpa_sigmoid")
+    if g == "sdpa_sigmoid":
+        return True
+    if g == "none":
+        return False
+    raise ValueError(f"unknown attention gate {g}")
+
+
+def parse_ts_config(text: str):
+    """A TimestralConfig from a config.json document (TimestralConfig.fromJson)."""
+    from .timestral_model import TimestralConfig
+
+    c = _parse_object(text)
+    _require_known(c, _TS_KEYS)
+    for key in ("attn_bias", "mlp_bias", "stabilize_with_global"):
+        if _bool(c, key, False):
+            raise ValueError(f"{key} = true is not supported")
+    sched = c.get("block_schedule")
+    if not isinstance(sched, list):
+        raise ValueError("block_schedule must be a list")
+    layers = []
+    for kind in sched:
+        if kind not in _TS_KINDS:
+            raise ValueError(f"unknown layer kind {kind}")
+        layers.append(_TS_KINDS[kind])
+    knots = c.get("quantile_knots")
+    if not isinstance(knots, list) or not all(_is_num(q) for q in knots):
+        raise ValueError("quantile_knots must be a list of numbers")
+    f32 = lambda v: float(np.float32(v))  # noqa: E731  (the reference keeps these as float)
+    cfg = TimestralConfig(
+        patch_size=_int(c, "patch_size", 0), d_model=_int(c, "d_model", 0), num_heads=_int(c, "num_heads", 0),
+        mlp_hidden_dim=_int(c, "mlp_hidden_dim", 0), layers=tuple(layers), quantiles=tuple(float(q) for q in knots),
+        rope_theta=f32(_num(c, "rope_theta", 10000.0)), rope_partial_factor=f32(_num(c, "rope_partial_factor", 0.5)),
+        norm_eps=f32(_num(c, "norm_eps", 1e-6)), time_attn_gate=_ts_gate(c, "time_attn_gate"),
+        variate_attn_gate=_ts_gate(c, "variate_attn_gate"), minimum_scale=f32(_num(c, "minimum_scale", 1e-6)),
+        use_asinh=_bool(c, "use_asinh", True), quantile_width_factor=f32(_num(c, "quantile_width_factor", 2.0)),
+        covariate_enabled=_bool(c, "covariate_enabled", True),
+        attend_missing=_bool(c, "attend_missing_patches", True), block_size=_int(c, "block_size", 0),
+        context_length=_int(c, "context_length", 0))
+    _ts_validate(cfg)
+    return cfg
+
+
+def _ts_validate(c) -> None:
+    """TimestralConfig.validate (TimestralConfig.java:211-227)."""
+    if c.patch_size < 1 or c.d_model < 1 or c.num_heads < 1 or c.d_model % c.num_heads:
+        raise ValueError(f"d_model {c.d_model} is not divisible by num_heads {c.num_heads}")
+    if c.rope_dim <= 0 or c.rope_dim % 2:
+        raise ValueError(f"rope_partial_factor {c.rope_partial_factor} gives rope_dim {c.rope_dim}")
+    for i in range(1, len(c.quantiles)):
+        if not c.quantiles[i - 1] < c.quantiles[i]:
+            raise ValueError("quantile_knots must be increasing")
+    if 0.5 not in c.quantiles:
+        raise ValueError("no 0.5 quantile knot")
+    if c.context_length % c.patch_size:
+        raise ValueError("context_length must be a multiple of patch_size")
+
+
+def ts_config_json(c) -> str:
+    """The config.json document of a TimestralConfig."""
+    kinds = {v: k for k, v in _TS_KINDS.items()}
+    doc = {
+        "patch_size": c.patch_size, "d_model": c.d_model, "num_heads": c.num_heads, "mlp_hidden_dim": c.mlp_hidden_dim,
+        "block_schedule": [kinds[tuple(bool(x) for x in axes)] for axes in c.layers],
+        "quantile_knots": list(c.quantiles), "block_size": c.block_size, "context_length": c.context_length,
+        "rope_theta": c.rope_theta, "rope_partial_factor": c.rope_partial_factor, "norm_eps": c.norm_eps,
+        "attn_bias": False, "mlp_bias": False, "time_attn_gate": "sdpa_sigmoid" if c.time_attn_gate else "none",
+        "variate_attn_gate": "sdpa_sigmoid" if c.variate_attn_gate else "none", "minimum_scale": c.minimum_scale,
+        "use_asinh": c.use_asinh, "covariate_enabled": c.covariate_enabled,
+        "attend_missing_patches": c.attend_missing, "quantile_width_factor": c.quantile_width_factor,
+    }
+    return json.dumps(doc, indent=2)
+
+
+def _timestral_names(c) -> list:
+    """(name, shape, key) of every tensor a Timestral checkpoint holds, in binding order
+    (TimestralWeights.java:92-117); key says where HipTimestralModel's weight dict keeps it."""
+    d, p, f = c.d_model, c.patch_size, c.mlp_hidden_dim
+    out = []
+
+    def residual(prefix, key, din, hidden, dout, bias):
+        for part, short, shp in (("hidden_layer", "hidden", (hidden, din)), ("output_layer", "output", (dout, hidden)),
+                                 ("residual_layer", "residual", (dout, din))):
+            out.append((f"{prefix}.{part}.weight", shp, f"{key}_{short}_w"))
+            if bias:
+                out.append((f"{prefix}.{part}.bias", (shp[0],), f"{key}_{short}_b"))
+
+    residual("representation.patch_proj", "embed", 2 * p, 4 * d, d, True)
+    out.append(("representation.forecast_query", (d,), "query"))
+    for i, axes in enumerate(c.layers):
+        s = f"transformer.layers.{i}"
+        for a, time in enumerate(axes):
+            gated = c.time_attn_gate if time else c.variate_attn_gate
+            out.append((f"{s}.attn_norms.{a}.scale", (d,), (i, a, "norm")))
+            out.append((f"{s}.attns.{a}.wQKV.weight", (3 * d, d), (i, a, "qkv")))
+            if gated:
+                out.append((f"{s}.attns.{a}._gate.weight", (d, d), (i, a, "gate")))
+            out.append((f"{s}.attns.{a}.wO.weight", (d, d), (i, a, "wo")))
+        out.append((f"{s}.mlp_norm.scale", (d,), (i, None, "mlp_norm")))
+        out.append((f"{s}.mlp.w12.weight", (2 * f, d), (i, None, "up")))
+        out.append((f"{s}.mlp.w3.weight", (d, f), (i, None, "down")))
+    out.append(("transformer.out_norm.scale", (d,), "out_norm"))
+    residual("head.projection", "head", d, 4 * d, p * c.num_quantiles, False)
+    return out
+
+
+def _qkv_heads_major(c, w: np.ndarray) -> np.ndarray:
+    """TimestralWeights.qkv: checkpoint row s*d + e*heads + h to engine row s*d + h*dh + e."""
+    d, heads, dh = c.d_model, c.num_heads, c.head_dim
+    return np.ascontiguousarray(w.reshape(3, dh, heads, d).transpose(0, 2, 1, 3).reshape(3 * d, d))
+
+
+def _qkv_checkpoint(c, w: np.ndarray) -> np.ndarray:
+    d, heads, dh = c.d_model, c.num_heads, c.head_dim
+    return np.ascontiguousarray(w.reshape(3, heads, dh, d).transpose(0, 2, 1, 3).reshape(3 * d, d))
+
+
+def _swap_halves(w: np.ndarray) -> np.ndarray:
+    """TimestralWeights.mlpUp: the two halves of w12 exchanged (its own inverse)."""
+    f = w.shape[0] // 2
+    return np.ascontiguousarray(np.concatenate([w[f:], w[:f]]))
+
+
+def load_timestral(checkpoint_dir) -> tuple:
+    """TimestralWeights.load: (TimestralConfig, weights) from <dir>/config.json and
+    <dir>/model.safetensors, the weights in HipTimestralModel's layout (see random_weights)."""
+    d = Path(checkpoint_dir)
+    c = parse_ts_config((d / "config.json").read_text(encoding="utf-8"))
+    with SafeTensors(d / "model.safetensors") as st:
+        bound: set = set()
+        w: dict = {"layers": [{"attentions": [{"time": bool(t), "gate": None} for t in axes]} for axes in c.layers]}
+        for name, shape, key in _timestral_names(c):
+            if name in bound:
+                raise RuntimeError(f"{name} bound twice")
+            bound.add(name)
+            if name not in st:
+                raise ValueError(f"checkpoint has no tensor {name}")
+            arr = st.get(name).require_f32(*shape).to_numpy()
+            if isinstance(key, tuple):
+                layer, a, k = key
+                if k == "qkv":
+                    arr = _qkv_heads_major(c, arr)
+                elif k == "up":
+                    arr = _swap_halves(arr)
+                (w["layers"][layer] if a is None else w["layers"][layer]["attentions"][a])[k] = arr
+            else:
+                w[key] = arr
+        unbound = sorted(set(st.tensors) - bound)
+        if unbound:
+            raise ValueError(f"unexpected tensors in checkpoint: {unbound}")
+    return c, w
+
+
+def write_timestral(checkpoint_dir, c, weights: dict) -> Path:
+    """Writes config.json and model.safetensors for weights in HipTimestralModel's layout."""
+    d = Path(checkpoint_dir)
+    d.mkdir(parents=True, exist_ok=True)
+    (d / "config.json").write_text(ts_config_json(c), encoding="utf-8")
+    tensors = {}
+    for name, _shape, key in _timestral_names(c):
+        if isinstance(key, tuple):
+            layer, a, k = key
+            arr = (weights["layers"][layer] if a is None else weights["layers"][layer]["attentions"][a])[k]
+            if k == "qkv":
+                arr = _qkv_checkpoint(c, np.asarray(arr, np.float32))
+            elif k == "up":
+                arr = _swap_halves(np.asarray(arr, np.float32))
+        else:
+            arr = weights[key]
+        tensors[name] = np.ascontiguousarray(arr, np.float32)
+    write_safetensors(d / "model.safetensors", tensors)
     return d

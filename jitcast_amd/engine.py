@@ -6,9 +6,12 @@ TornadoChronos2Engine is over Chronos2Forward (J/chronos2/tornado/TornadoChronos
                       the encoder, finish), eager or replayed from a plan per batch shape
   HipChronos2Engine   load(checkpoint_dir) / forecast(series, horizon) / name() / close(); config(),
                       forward_pass() and pipeline() as the reference's engine exposes them
+  HipTimestralEngine  the same over TimestralPipeline (ts_pipeline.py) and HipTimestralModel.predict_block,
+                      as TornadoTimestralEngine (J/timestral/tornado/TornadoTimestralEngine.java:29-111)
 
 Settings come from the arguments or, when an argument is None, from the -D properties (options.py):
-chronos2.hip.dtype, chronos2.hip.plans, chronos2.hip.planBytes, jitcast.hip.device.
+chronos2.hip.dtype, chronos2.hip.plans, chronos2.hip.planBytes, timestral.hip.dtype,
+timestral.hip.plans, timestral.hip.planBytes, timestral.hip.buckets, jitcast.hip.device.
 """
 from __future__ import annotations
 
@@ -108,3 +111,64 @@ class HipChronos2Engine(ForecastEngine):
             self._closed = True
             self._forward.close()
             self._forward.model = None
+
+
+class HipTimestralEngine(ForecastEngine):
+    """Timestral on one GPU: TimestralPipeline around HipTimestralModel.predict_block. The engine owns its
+    weights (uploaded once) and releases them in close(); calls from several threads run one at a time."""
+
+    def __init__(self, config, weights: dict, dtype: str | None = None, device: int | None = None,
+                 max_plans: int | None = None, plan_bytes: int | None = None, buckets: bool | None = None,
+                 pipeline_options=None, batch_size: int | None = None, max_tokens: int | None = None):
+        from .timestral_model import HipTimestralModel
+        from .ts_pipeline import DEFAULT_BATCH_SIZE, TimestralPipeline
+
+        dtype = dtype if dtype is not None else opts.choice("timestral.hip.dtype", "f32", "f32", "bf16", "fp16")
+        if dtype not in ("f32", "bf16", "fp16"):
+            raise ValueError(f"dtype must be f32, bf16 or fp16, got {dtype}")
+        device = device if device is not None else opts.integer("jitcast.hip.device", 0, 0)
+        self._config = config
+        self._dtype = dtype
+        self._model = HipTimestralModel(config, weights, dtype=dtype, device=device, max_plans=max_plans,
+                                        plan_bytes=plan_bytes, buckets=buckets)
+        self._pipeline = TimestralPipeline(config, self._model.predict_block, pipeline_options,
+                                           batch_size if batch_size is not None else DEFAULT_BATCH_SIZE, max_tokens)
+        self._lock = threading.Lock()
+        self._closed = False
+
+    @staticmethod
+    def load(checkpoint_dir, **kw) -> "HipTimestralEngine":
+        """An engine over <dir>/config.json and <dir>/model.safetensors (TornadoTimestralEngine.load); the
+        load fails on unknown config keys, unsupported settings and missing, misshapen or extra tensors."""
+        from .checkpoint import load_timestral
+
+        config, weights = load_timestral(checkpoint_dir)
+        return HipTimestralEngine(config, weights, **kw)
+
+    def config(self):
+        return self._config
+
+    def forward_pass(self):
+        """The device block forward under the pipeline (HipTimestralModel), for benchmarks and tests."""
+        return self._model
+
+    def pipeline(self):
+        """The host pipeline forecast() runs; its with_* methods give pipelines with other settings over
+        this engine's forward pass."""
+        return self._pipeline
+
+    def forecast(self, series: list, horizon: int) -> list:
+        with self._lock:
+            if self._closed:
+                raise RuntimeError("the engine is closed")
+            return self._pipeline.forecast(series, horizon)
+
+    def name(self) -> str:
+        return "timestral-hip" if self._dtype == "f32" else f"timestral-hip-{self._dtype}"
+
+    def close(self) -> None:
+        with self._lock:
+            if self._closed:
+                return
+            self._closed = True
+            self._model.close()

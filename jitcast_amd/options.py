@@ -11,6 +11,9 @@ Properties read by this package:
                             f16x3 keeps fp32 results with the GEMMs on three-term fp16 splits (f32)
   chronos2.hip.plans        plans cached per engine, one hipGraph per batch shape; 0 runs eagerly (8)
   chronos2.hip.planBytes    device bytes the cached plans may hold (the device's memory)
+  timestral.maxTokens       tokens (rows x patches) per Timestral forward pass before the pipeline
+                            splits a call into windows (131072)
+  timestral.hip.dtype       f32 | bf16 | fp16: the Timestral engine's GEMM and attention type (f32)
   timestral.hip.buckets     pad blocks to shared shapes before the forward (true)
   timestral.hip.plans       plans cached per HipTimestralModel, one hipGraph per block shape; 0 runs
                             eagerly (8)

@@ -58,6 +58,7 @@ class TimestralConfig:
     covariate_enabled: bool = True
     attend_missing: bool = True
     block_size: int = 64
+    context_length: int = 16384  # steps the pipeline keeps by default (Options.maxContext)
 
     @property
     def head_dim(self) -> int:
@@ -74,6 +75,14 @@ class TimestralConfig:
     @property
     def median_index(self) -> int:
         return self.quantiles.index(0.5)
+
+    def supports_known_covariates(self) -> bool:
+        """TimestralConfig.supportsKnownCovariates (TimestralConfig.java:129-148): covariates on, and a time
+        attention followed later by both a time and a variate attention."""
+        if not self.covariate_enabled:
+            return False
+        ops = [bool(t) for axes in self.layers for t in axes]
+        return any(ops[i] and True in ops[i + 1:] and False in ops[i + 1:] for i in range(len(ops)))
 
 
 def random_weights(c: TimestralConfig, seed: int = 0, std: float = 0.02) -> dict:
@@ -302,7 +311,16 @@ class HipTimestralModel:
         inputs / observed [rows, t] (t a multiple of the patch), group [rows] with each series' rows
         contiguous, h forecast patches, role [rows] (0 TARGET, 1 PAST, 2 KNOWN) and the known
         covariates' future steps [rows, h*P] for a covariate block. Returns [rows, h*P, Q]
-        quantiles."""
+        quantiles. With plans, the whole block (uploads, prep, replay, finish, download) runs on the
+        model's stream, so every launch and copy of it is ordered on that one stream."""
+        import torch
+
+        if self.plans is not None:
+            with torch.cuda.stream(self._stream):
+                return self._predict(inputs, observed, group, h, role, known_future, known_future_mask)
+        return self._predict(inputs, observed, group, h, role, known_future, known_future_mask)
+
+    def _predict(self, inputs, observed, group, h: int, role, known_future, known_future_mask):
         import torch
 
         c = self.c
@@ -336,6 +354,7 @@ class HipTimestralModel:
             raw = self.forward_raw(tok, kv_d, known_d, pos_d, gs_d, ge_d, role_d, cov, rows, enc, h)
         out = torch.empty(rows, h * ps, q, dtype=torch.float32, device=dev)
         widths = quantile_widths(c)
+        ctx = chronos2.context(dev.index or 0)  # bound again: a capture above binds the context too
         _lib.call("jc_ts_finish", ctx.handle, p(raw), p(loc), p(scale), rows, wlen, t // ps, h, ps, q,
                   widths.ctypes.data, c.median_index, int(c.use_asinh), p(out))
         return out.cpu().numpy()
@@ -344,26 +363,21 @@ class HipTimestralModel:
     def _forward_planned(self, tok, kv, known, pos, gs, ge, role, cov: bool, rows: int, enc: int, h: int):
         """The forward replayed from the plan of Shape(rows, encoder, horizon, covariates)
         (TimestralForward.predictExact's plans.run): the per-call inputs copied into the plan's buffers,
-        then its captured forward on the model's stream; returns the plan's raw output."""
-        import torch
-
+        then its captured forward; returns the plan's raw output. Runs on the model's stream, which
+        predict_exact makes current."""
         shape = (rows, enc, h, bool(cov))
-        cur = torch.cuda.current_stream(self.dev)
-        self._stream.wait_stream(cur)
 
         def use(plan):
             b = plan.bufs
-            with torch.cuda.stream(self._stream):
-                b["tok"].copy_(tok)
-                b["kv"].copy_(kv)
-                b["known"].copy_(known)
-                b["pos"].copy_(pos)
-                b["gs"].copy_(gs)
-                b["ge"].copy_(ge)
-                if role is not None:
-                    b["role"].copy_(role)
-                plan.graph.launch()
-            cur.wait_stream(self._stream)
+            b["tok"].copy_(tok)
+            b["kv"].copy_(kv)
+            b["known"].copy_(known)
+            b["pos"].copy_(pos)
+            b["gs"].copy_(gs)
+            b["ge"].copy_(ge)
+            if role is not None:
+                b["role"].copy_(role)
+            plan.graph.launch()
             return b["raw"]
 
         return self.plans.run(shape, self._capture, use)
