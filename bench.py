@@ -482,6 +482,61 @@ def forecast_line(ckpt_dir, series, n_targets: int, dtype_name: str = "f32", cpu
     return res
 
 
+def ts_forecast_line(dtype_name: str = "f32", rows: int = 64, steps: int = 16384, horizon: int = 64) -> dict:
+    """The Timestral engine end to end: HipTimestralEngine.load(config.json + model.safetensors of the
+    123M-class random-init model, the shape of config 3's stack with its MLPs and head), then
+    ForecastEngine.forecast of `rows` univariate series of `steps` steps (config 0's sines + trend +
+    noise; 16,384 steps are config 3's 1,024 patch tokens) at `horizon`, sign-flip averaging on (two
+    block calls). value = series forecast per second from the median forecast() wall time
+    (Chronos2Bench's method), from plans (the default) and eagerly; both must agree bit for bit."""
+    import shutil
+    import tempfile
+
+    import numpy as np
+
+    from jitcast_amd import checkpoint, synthetic
+    from jitcast_amd import timestral_model as tm
+    from jitcast_amd.api import TimeSeries
+    from jitcast_amd.engine import HipTimestralEngine
+
+    c = tm.TimestralConfig()
+    x = synthetic.c2_config0_series(rows, steps, seed=3)
+    series = [TimeSeries.univariate(r) for r in x]
+    ckpt = Path(tempfile.mkdtemp(prefix="ts_engine_"))
+    try:
+        log(f"writing the Timestral 123M-class random-init checkpoint ({dtype_name} engine)")
+        checkpoint.write_timestral(ckpt, c, tm.random_weights(c, seed=0, std=0.02))
+        res = {}
+        for plans in (8, 0):
+            with HipTimestralEngine.load(ckpt, dtype=dtype_name, max_plans=plans) as eng:
+                calls = []
+                fwd = eng.pipeline().forward
+                eng.pipeline().forward = lambda inp, *a: calls.append(np.shape(inp)) or fwd(inp, *a)
+                out = eng.forecast(series, horizon)
+                eng.pipeline().forward = fwd
+                res[plans] = (out, chronos2_bench_timing(lambda: eng.forecast(series, horizon), budget_s=4.0), calls)
+    finally:
+        shutil.rmtree(ckpt, ignore_errors=True)
+    (out, t, calls), (eout, te, _) = res[8], res[0]
+    assert all(np.array_equal(a.values, b.values) for a, b in zip(out, eout)), "plan replay differs from eager"
+    assert all(np.isfinite(f.values).all() for f in out)
+    sps = rows / (t["median_ms"] * 1e-3)
+    log(f"timestral forecast {dtype_name} through the engine: median {t['median_ms']:.1f} ms per forecast() of "
+        f"{rows} series ({len(calls)} block calls of {calls[0]}), {sps:.0f} series/s; eager "
+        f"{te['median_ms']:.1f} ms")
+    return {
+        "workload": f"Timestral 123M-class forecast() through HipTimestralEngine ({dtype_name}), {rows} univariate "
+                    f"series x {steps} steps, horizon {horizon}, 9 quantiles, sign-flip averaging, random-init "
+                    "weights loaded from config.json + model.safetensors",
+        "metric": "forecast series/sec",
+        "value": round(sps, 1),
+        "unit": "series/s",
+        "timing": t,
+        "block_calls": len(calls), "block_shape": list(calls[0]),
+        "eager_timing": te, "eager_series_per_s": round(rows / (te["median_ms"] * 1e-3), 1),
+    }
+
+
 def forecast_cpu_baseline(ckpt_dir, series, threads: int, groups: int = 4) -> dict:
     """The oracle (CpuChronos2.forward under ModelLayout, ModelPrep and finish) on one forward call of
     `groups` config-4 series (5 rows each), scaled linearly to target series per second: without
@@ -571,7 +626,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=256)
-    ap.add_argument("--only", choices=["all", "time", "group", "bf16", "fp16", "layer", "layer-bf16", "layer-f16x3", "ts", "ts-block", "ts-block-bf16", "forecast"], default="all",
+    ap.add_argument("--only", choices=["all", "time", "group", "bf16", "fp16", "layer", "layer-bf16", "layer-f16x3", "ts", "ts-block", "ts-block-bf16", "ts-forecast", "forecast"], default="all",
                     help="which workloads to run (profiling runs select one kernel)")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="only run 5 plain device copies of this many bytes (calibrates rocprof byte counters)")
@@ -620,6 +675,12 @@ def main() -> int:
         finally:
             shutil.rmtree(ckpt, ignore_errors=True)
         if args.only == "forecast":
+            print(json.dumps({"also": also}), flush=True)
+            return 0
+    if args.only in ("all", "ts-forecast"):
+        for name in ("bf16", "f32"):
+            also[f"ts_forecast_{name}"] = ts_forecast_line(name)
+        if args.only == "ts-forecast":
             print(json.dumps({"also": also}), flush=True)
             return 0
     if args.only in ("all", "ts-block", "ts-block-bf16"):

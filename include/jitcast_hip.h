@@ -261,6 +261,30 @@ int jc_ts_block_layout(const uint8_t *observed, const uint8_t *future_observed, 
                        int attend_missing, int block_size, int *enc_out, int *covariates_out, int32_t *key_valid,
                        int32_t *known, int32_t *pos);
 
+/*
+ * Per row of Timestral's assembled context x [rows][t] with observed [rows][t] 0/1, host memory:
+ * Scaler.lastLocScale (J/timestral/Scaler.java:65-79), the mean (loc) and Bessel-corrected std
+ * (scale, at least minimum_scale) of the observed values, summed in double in order; and the
+ * smallest (lo) and largest (hi) observed value, 0 when none is, which TimestralPipeline's cap
+ * bounds use (_cap_quantiles, TimestralPipeline.java:378-395). NaN propagates. Outputs [rows];
+ * any may be NULL.
+ */
+int jc_ts_context_stats(const float *x, const uint8_t *observed, int rows, int t, float minimum_scale, float *loc,
+                        float *scale, float *lo, float *hi);
+
+/*
+ * Scaler.advancingFrames (J/timestral/Scaler.java:161-236), host memory: the (loc, scale) frame of
+ * each of a decoded block's n_pred patches, patch j in the statistics of the observed context
+ * plus the block's medians of patches 0..j-1 (each denormalised in its own frame, clipped and
+ * folded in by welford_combine). The context's per-patch states combine by an inclusive
+ * Hillis-Steele scan in the reference's order.
+ *   context, observed  [rows][t], t a multiple of patch, t >= patch
+ *   sinh_median        [rows][n_pred][patch] (median - loc) / scale in the last context patch's frame
+ *   locs, scales       out [rows][n_pred], double
+ */
+int jc_ts_advancing_frames(const float *context, const uint8_t *observed, const double *sinh_median, int rows, int t,
+                           int patch, int n_pred, float minimum_scale, double *locs, double *scales);
+
 /* ---- The Chronos-2 encoder layer around the attention cores (fp32) -------------------------- */
 
 /* Kernels.gemm flags (J/tornado/Kernels.java:50-56). */

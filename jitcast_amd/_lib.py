@@ -94,6 +94,8 @@ SIGNATURES = {
     "jc_c2_residual": (_i, [_vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp]),
     "jc_ts_block_layout": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _c.POINTER(_i), _c.POINTER(_i), _vp,
                                 _vp, _vp]),
+    "jc_ts_context_stats": (_i, [_vp, _vp, _i, _i, _f, _vp, _vp, _vp, _vp]),
+    "jc_ts_advancing_frames": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _f, _vp, _vp]),
 }
 
 _lib = None

@@ -23,11 +23,13 @@ the reference runs in order run in order here, across rows at once.
 """
 from __future__ import annotations
 
+import ctypes
 import math
 from dataclasses import dataclass, replace
 
 import numpy as np
 
+from . import _lib
 from . import options as opts
 from .api import Forecast, TimeSeries
 
@@ -173,92 +175,46 @@ def target_encode(ts: TimeSeries, horizon: int, max_context: int) -> TimeSeries:
 
 # ---- Scaler ------------------------------------------------------------------------------------
 
+def context_stats(x: np.ndarray, observed: np.ndarray, minimum_scale: float):
+    """(loc, scale, lo, hi) float32 [rows] of each row (jc_ts_context_stats): Scaler.lastLocScale's
+    causal mean and Bessel-corrected std of every observed value (a running sum in double, in order)
+    and the smallest and largest observed value (0 when none is)."""
+    x = np.ascontiguousarray(np.atleast_2d(x), np.float32)
+    m = np.ascontiguousarray(np.atleast_2d(observed), np.uint8)
+    rows, t = x.shape
+    if m.shape != x.shape:
+        raise ValueError(f"observed {m.shape} does not match the values {x.shape}")
+    out = [np.empty(rows, np.float32) for _ in range(4)]
+    _lib.call("jc_ts_context_stats", x.ctypes.data, m.ctypes.data, rows, t, ctypes.c_float(minimum_scale),
+              *(o.ctypes.data for o in out))
+    return tuple(out)
+
+
 def last_loc_scale(x: np.ndarray, observed: np.ndarray, minimum_scale: float):
-    """(loc, scale) float32 [rows] of each row's last patch: the causal mean and Bessel-corrected std
-    of every observed value (a running Welford in double, in order)."""
-    x = np.atleast_2d(np.asarray(x, np.float32)).astype(np.float64)
-    w = np.atleast_2d(observed).astype(np.float64)
-    cum_w = np.cumsum(w, axis=1)
-    mean = np.cumsum(w * x, axis=1) / np.maximum(cum_w, 1.0)
-    prev = np.concatenate([np.zeros((x.shape[0], 1)), mean[:, :-1]], axis=1)
-    m2 = np.cumsum((x - prev) * (x - mean) * w, axis=1)[:, -1]
-    var = m2 / np.maximum(np.maximum(cum_w[:, -1], 1.0) - 1.0, 1.0)
-    return mean[:, -1].astype(np.float32), np.maximum(np.sqrt(var), float(np.float32(minimum_scale))).astype(np.float32)
-
-
-def _combine(wa, ma, m2a, wb, mb, m2b):
-    """welford_combine of two (weight, mean, m2) states, element-wise; (0, 0, 0) is the identity."""
-    w = wa + wb
-    w_safe = np.maximum(w, np.finfo(np.float64).tiny)
-    delta = mb - ma
-    mean = ma + delta * wb / w_safe
-    m2 = m2a + m2b + delta * delta * wa * wb / w_safe
-    zero = w == 0
-    return w, np.where(zero, 0.0, mean), np.where(zero, 0.0, m2)
+    """(loc, scale) float32 [rows] of each row's last patch: Scaler.lastLocScale
+    (Scaler.java:65-79), the causal mean and Bessel-corrected std of every observed value."""
+    loc, scale, _, _ = context_stats(x, observed, minimum_scale)
+    return loc, scale
 
 
 def advancing_frames(context: np.ndarray, observed: np.ndarray, sinh_median: np.ndarray, patch: int,
                      minimum_scale: float):
-    """(loc, scale) double [rows, H] of each decoded patch in the advancing refine frame: patch j uses
-    the statistics of the observed context plus the block's medians of patches 0..j-1, each folded in
-    after being denormalised in its own frame. context / observed [rows, T] (T a multiple of the
-    patch), sinh_median [rows, H, patch] (median - loc) / scale of the last context patch."""
-    ctx = np.asarray(context, np.float32).astype(np.float64)
-    wv = np.asarray(observed).astype(np.float64)
+    """(loc, scale) double [rows, H] of each decoded patch in the advancing refine frame
+    (jc_ts_advancing_frames, Scaler.advancingFrames): patch j uses the statistics of the observed
+    context plus the block's medians of patches 0..j-1, each folded in after being denormalised in
+    its own frame. context / observed [rows, T] (T a multiple of the patch), sinh_median
+    [rows, H, patch] (median - loc) / scale of the last context patch."""
+    ctx = np.ascontiguousarray(context, np.float32)
+    m = np.ascontiguousarray(observed, np.uint8)
+    sm = np.ascontiguousarray(sinh_median, np.float64)
     rows, t = ctx.shape
-    n_pred = sinh_median.shape[1]
-    n_ctx = t // patch
-    n = n_ctx + n_pred
-    cw = ctx.reshape(rows, n_ctx, patch)
-    ww = wv.reshape(rows, n_ctx, patch)
-    cnt = np.zeros((rows, n_ctx))
-    s = np.zeros((rows, n_ctx))
-    for i in range(patch):  # in order, as the reference sums a patch
-        cnt = cnt + ww[:, :, i]
-        s = s + cw[:, :, i] * ww[:, :, i]
-    mu = s / np.maximum(cnt, 1.0)
-    s2 = np.zeros((rows, n_ctx))
-    for i in range(patch):
-        dv = cw[:, :, i] - mu
-        s2 = s2 + ww[:, :, i] * (dv * dv)
-    w = np.zeros((rows, n))
-    mean = np.zeros((rows, n))
-    m2 = np.zeros((rows, n))
-    w[:, :n_ctx] = cnt
-    mean[:, :n_ctx] = np.where(cnt == 0, 0.0, mu)
-    m2[:, :n_ctx] = np.where(cnt == 0, 0.0, s2)
-    d = 1
-    while d < n:  # cumulative_welford: an inclusive Hillis-Steele scan
-        za = np.zeros((rows, d))
-        wa = np.concatenate([za, w[:, :-d]], axis=1) if d < n else np.zeros_like(w)
-        ma = np.concatenate([za, mean[:, :-d]], axis=1) if d < n else np.zeros_like(w)
-        m2a = np.concatenate([za, m2[:, :-d]], axis=1) if d < n else np.zeros_like(w)
-        w, mean, m2 = _combine(wa, ma, m2a, w, mean, m2)
-        d *= 2
-    k = n - n_pred - 1
-    c_w, c_mu, c_m2 = w[:, k].copy(), mean[:, k].copy(), m2[:, k].copy()
-    offset = c_mu.copy()
-    clip = math.sqrt(_F32_MAX) / 1e3
-    min_s = float(np.float32(minimum_scale))
-    locs = np.zeros((rows, n_pred))
-    scales = np.zeros((rows, n_pred))
-    for h in range(n_pred):
-        var = np.maximum(c_m2 / np.maximum(c_w - 1.0, 1.0), 0.0)
-        sc = np.maximum(np.sqrt(var), min_s)
-        locs[:, h] = c_mu
-        scales[:, h] = sc
-        folded = np.empty((rows, patch))
-        tot = np.zeros(rows)
-        for i in range(patch):
-            fv = np.maximum(-clip, np.minimum(clip, sinh_median[:, h, i] * sc + c_mu - offset))
-            folded[:, i] = fv + offset
-            tot = tot + folded[:, i]
-        b_mean = tot / patch
-        b_m2 = np.zeros(rows)
-        for i in range(patch):
-            dv = folded[:, i] - b_mean
-            b_m2 = b_m2 + dv * dv
-        c_w, c_mu, c_m2 = _combine(c_w, c_mu, c_m2, np.full(rows, float(patch)), b_mean, b_m2)
+    n_pred = sm.shape[1]
+    if m.shape != ctx.shape or sm.shape != (rows, n_pred, patch):
+        raise ValueError(f"shapes disagree: context {ctx.shape}, observed {m.shape}, sinh_median {sm.shape}")
+    locs = np.empty((rows, n_pred))
+    scales = np.empty((rows, n_pred))
+    _lib.call("jc_ts_advancing_frames", ctx.ctypes.data, m.ctypes.data, sm.ctypes.data, rows, t, patch, n_pred,
+              ctypes.c_float(minimum_scale), locs.ctypes.data, scales.ctypes.data)
     return locs, scales
 
 
@@ -316,6 +272,8 @@ def non_negative(row: np.ndarray) -> bool:
 
 def forward_fill(x: np.ndarray, m: np.ndarray) -> np.ndarray:
     """ffill_with_mask: unobserved positions take the last observed value; leading ones take x[0]."""
+    if m.all():  # nothing to fill
+        return np.asarray(x, np.float32)
     idx = np.where(m, np.arange(x.size), -1)
     last = np.maximum.accumulate(idx)
     return np.where(m, x, np.where(last >= 0, x[np.maximum(last, 0)], x[0])).astype(np.float32)
@@ -461,13 +419,13 @@ class TimestralPipeline:
         c = self.config
         a = self.assemble(series, horizon, sign)
         q = self._decode(a, horizon)
+        bounds = self._cap_bounds(a.rows, a.mask)
         out = []
         for s in range(len(series)):
             tr = a.target_rows[s]
             f = np.transpose(q[tr], (0, 2, 1)).copy()  # [targets][Q][horizon]
-            b = self._cap_bounds(a.rows[tr], a.mask[tr])
-            if b is not None:
-                lo, hi = b[0][:, None, None], b[1][:, None, None]
+            if bounds is not None:
+                lo, hi = bounds[0][tr][:, None, None], bounds[1][tr][:, None, None]
                 f = np.minimum(np.maximum(f, lo), hi)  # Math.min(Math.max(x, b0), b1): NaN kept
             if np.isnan(f).any():
                 raise RuntimeError("forecast produced NaN values: the input is degenerate, or an activation left "
@@ -476,15 +434,13 @@ class TimestralPipeline:
         return out
 
     def _cap_bounds(self, rows: np.ndarray, mask: np.ndarray):
-        """_cap_quantiles: [min - k s, max + k s] of each row's observed context (float32), or None."""
+        """_cap_quantiles (TimestralPipeline.java:378-395): [min - k s, max + k s] of each row's observed
+        context (float32), or None."""
         o = self._options
         if o.cap_k <= 0:
             return None
-        mx = np.where(mask, rows, -np.inf).max(axis=1)
-        mn = np.where(mask, rows, np.inf).min(axis=1)
-        mx = np.where(mx == -np.inf, f32(0), mx).astype(np.float32)
-        mn = np.where(mn == np.inf, f32(0), mn).astype(np.float32)
-        s = last_loc_scale(rows, mask, self.config.minimum_scale)[1] * f32(o.cap_k)
+        _, scale, mn, mx = context_stats(rows, mask, self.config.minimum_scale)
+        s = scale * f32(o.cap_k)
         return (mn - s).astype(np.float32), (mx + s).astype(np.float32)
 
     def _decode(self, a: Assembled, horizon: int) -> np.ndarray:

@@ -94,6 +94,39 @@ def test_advancing_frames_recomputed_two_pass():
             vals += list(sinh[i, h] * sd + mu)
 
 
+def test_native_statistics_equal_the_scalar_loops():
+    """jc_ts_context_stats and jc_ts_advancing_frames (the library's host helpers behind last_loc_scale,
+    the cap range and advancing_frames) against the restatement's scalar loops, value for value, on
+    rows with gaps, NaN and +-inf, unobserved rows, one-step patches and scales from 1e-3 to 1e20
+    (NaN compared as NaN, +0 and -0 as equal)."""
+    r = np.random.default_rng(7)
+    for trial in range(120):
+        rows, patch = int(r.integers(1, 5)), int(r.choice([1, 2, 4, 16]))
+        t = patch * int(r.integers(1, 30))
+        x = (r.standard_normal((rows, t)) * r.choice([1e-3, 1, 1e3, 1e20])).astype(np.float32) + f32(r.standard_normal())
+        obs = r.random((rows, t)) > r.choice([0.0, 0.3, 0.9, 1.0])
+        if trial % 7 == 0:
+            x[r.random((rows, t)) < 0.05] = np.nan
+        if trial % 11 == 0:
+            x[r.random((rows, t)) < 0.05] = np.inf
+        ms = float(r.choice([1e-6, 1e-3, 0.5]))
+        loc, scale, lo, hi = tp.context_stats(x, obs, ms)
+        for i in range(rows):
+            want = ref.last_loc_scale(x[i], obs[i], ms)
+            np.testing.assert_array_equal([loc[i], scale[i]], np.asarray(want, np.float32))
+            seen = x[i][obs[i]]
+            np.testing.assert_array_equal([lo[i], hi[i]], [seen.min() if seen.size else 0, seen.max() if seen.size else 0])
+        n_pred = int(r.integers(1, 6))
+        sinh = r.standard_normal((rows, n_pred, patch)) * r.choice([1, 1e3, 1e30])
+        if trial % 5 == 0:
+            sinh[0, 0, 0] = np.nan
+        locs, scales = tp.advancing_frames(x, obs, sinh, patch, ms)
+        for i in range(rows):
+            want = ref.advancing_frames(x[i], obs[i], sinh[i], patch, ms)
+            np.testing.assert_array_equal(locs[i], want[0])
+            np.testing.assert_array_equal(scales[i], want[1])
+
+
 def test_forward_fill_and_clamp_non_finite():
     x = np.array([0, 0, 3, 0, 5, 0], np.float32)
     m = np.array([False, False, True, False, True, False])
