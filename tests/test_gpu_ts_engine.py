@@ -110,3 +110,95 @@ def test_capturing_forecast_equals_replayed(gpu, checkpoint, buckets):
     for a, b, e in zip(first, second, want):
         np.testing.assert_array_equal(a.values, e.values)
         np.testing.assert_array_equal(b.values, e.values)
+
+
+C_LONG = tm.TimestralConfig(patch_size=16, d_model=64, num_heads=2, mlp_hidden_dim=96,
+                            layers=((True, False), (True, False)), quantiles=(0.1, 0.3, 0.5, 0.7, 0.9))
+
+
+def _walk(r, rows: int, length: int) -> np.ndarray:
+    v = 10 * r.random((rows, 1))
+    steps = np.cumsum(0.3 * r.standard_normal((rows, length)), axis=1) + v
+    return (steps + 2 * np.sin(2 * np.pi * np.arange(length) / 24)).astype(np.float32)
+
+
+def _mixed_batch(seed: int, count: int, horizon: int) -> list:
+    """The shape of TimestralBatchParityAccelTest.batch (TimestralBatchParityAccelTest.java:75-104):
+    series of 40..939 steps, every fifth with two targets, late starts, gaps, past covariates on every
+    third and known-future covariates (a daily on/off pattern) on another third."""
+    r = np.random.default_rng(seed)
+    out = []
+    for s in range(count):
+        length = 40 + int(r.integers(900))
+        t = _walk(r, 2 if s % 5 == 0 else 1, length)
+        if s % 7 == 3:
+            t[0, :min(length, 50)] = np.nan  # a late start
+        if s % 4 == 1:
+            t[0, length // 3:length // 3 + 20] = np.nan  # a gap
+        past = _walk(r, 1 + int(r.integers(2)), length) if s % 3 == 1 else None
+        known = None
+        if s % 3 == 2:
+            row = ((np.arange(length + horizon) % 24) < 6).astype(np.float32)
+            known = np.stack([row] * (1 + int(r.integers(2))))
+        out.append(TimeSeries(t, past, known))
+    return out
+
+
+@pytest.fixture(scope="module")
+def long_checkpoint(tmp_path_factory):
+    d = tmp_path_factory.mktemp("tsckpt_long")
+    ck.write_timestral(d, C_LONG, tm.random_weights(C_LONG, seed=5, std=0.1))
+    return d
+
+
+@pytest.mark.parametrize("dtype,bar", [("f32", 1e-4), ("bf16", 5e-2)])
+def test_mixed_batch_calls_match_the_oracle_forward(gpu, oracle, long_checkpoint, dtype, bar):
+    """TimestralBatchParityAccelTest.mixedBatchMatchesTheCpuReference: 37 mixed series at horizon 1100
+    (several blocks per pass, both sign passes), every predict_block call of the engine's pipeline
+    against the oracle's block forward on the same inputs, within 1e-4 in fp32 and the reference's
+    REDUCED_TOLERANCE (5e-2) with reduced-precision GEMMs."""
+    horizon = 1100
+    series = _mixed_batch(11, 37, horizon)
+    c, w = ck.load_timestral(long_checkpoint)
+    calls = []
+    with HipTimestralEngine.load(long_checkpoint, dtype=dtype) as eng:
+        pipe = eng.pipeline()
+        fwd = pipe.forward
+
+        def rec(*a):
+            out = fwd(*a)
+            calls.append(([None if x is None else np.array(x, copy=True) for x in a], np.array(out, copy=True)))
+            return out
+
+        pipe.forward = rec
+        try:
+            got = eng.forecast(series, horizon)
+        finally:
+            pipe.forward = fwd
+    assert len(got) == len(series) and all(np.isfinite(f.values).all() for f in got)
+    ofwd = _oracle_forward(oracle, c, w, [])
+    worst = 0.0
+    for k, (args, out) in enumerate(calls):
+        x, obs, group, h, role, kf, kfm = args
+        err = oracle.rel_max_error(out, ofwd(x, obs, group, int(h), role, kf, kfm))
+        print(f"  mixed batch call{k} rows={x.shape[0]} length={x.shape[1]} horizon patches={int(h)} "
+              f"covariates={role is not None} rel max err {err:.2e}", flush=True)
+        worst = max(worst, err)
+    assert len(calls) >= 6 and worst <= bar
+
+
+def test_ragged_series_match_their_padded_batch(gpu, long_checkpoint):
+    """PipelineGoldenTest.raggedSeriesMatchTheirPaddedBatch: series passed at their own lengths forecast
+    as the same series left-padded with NaN to one length do (leading unobserved patches are never
+    keys and positions count from each series' first observation), within 1e-4."""
+    r = np.random.default_rng(4)
+    lengths = (300, 173, 64, 250, 97, 300)
+    ragged = [TimeSeries.univariate(_walk(r, 1, n)[0]) for n in lengths]
+    padded = [TimeSeries.univariate(np.concatenate([np.full(300 - s.length(), np.nan, np.float32), s.target[0]]))
+              for s in ragged]
+    with HipTimestralEngine.load(long_checkpoint, dtype="f32") as eng:
+        a = eng.forecast(ragged, 48)
+        b = eng.forecast(padded, 48)
+    err = max(float(np.max(np.abs(x.values - y.values)) / np.max(np.abs(y.values))) for x, y in zip(a, b))
+    print(f"  ragged vs padded forecasts rel max err {err:.2e}", flush=True)
+    assert err <= 1e-4
