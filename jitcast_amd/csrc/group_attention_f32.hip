@@ -29,6 +29,9 @@
 //                        from one 16-byte load per m and a 64-byte run per row per load.
 //   O^T[e][q] += V^T P^T: step c contracts key 4kk + c, whose P^T is S^T's reg c; V^T is loaded
 //                        per lane as V[key][e] (16 rows x 64 contiguous bytes per load).
+#include <algorithm>
+#include <cstdlib>
+
 #include "jc_common.hpp"
 #include "jc_kernels.hpp"
 
@@ -72,9 +75,14 @@ __global__ __launch_bounds__(kWave) void group_attention_f32(const GroupArgs a, 
     const int rows = a.rows, n = a.n, heads = a.heads, inner = a.inner;
     const int lane = threadIdx.x;
     const int j = lane % 16, g = lane / 16;
-    const uint32_t total = (uint32_t)a.rtiles * n;
+    const uint32_t total = (uint32_t)a.rtiles * n * a.hsplit;
     const uint32_t logical = xcd_remap(blockIdx.x, total);
-    const int t = logical / a.rtiles, rt = logical % a.rtiles;
+    const uint32_t tile_slot = logical / a.hsplit;
+    const int t = tile_slot / a.rtiles, rt = tile_slot % a.rtiles;
+    // this wave's heads [h_lo, h_hi): a (tile, slot)'s heads are split over hsplit waves, so the
+    // tiles where long groups start do not hold one wave for all heads while their neighbours idle
+    const int hs = logical % a.hsplit;
+    const int h_lo = heads * hs / a.hsplit, h_hi = heads * (hs + 1) / a.hsplit;
     const int r0 = rt * kRT;
     const int nr = min(kRT, rows - r0);
     const size_t stride = 3 * (size_t)inner;  // floats per token of qkv
@@ -96,8 +104,9 @@ __global__ __launch_bounds__(kWave) void group_attention_f32(const GroupArgs a, 
     const bool single = lane >= nr || (gs_l == r0 + lane && (ge_l <= r0 + lane + 1 || r0 + lane + 1 >= rows));
     if (__ballot(!single) == 0) {
         const int pj = lane % 16;  // 16 lanes per (row, head) pair, 4 dims each per 64-dim step
-        for (int pr = lane / 16; pr < nr * heads; pr += kWave / 16) {
-            const int row = r0 + pr / heads, h = pr % heads;
+        const int hn = h_hi - h_lo;
+        for (int pr = lane / 16; pr < nr * hn; pr += kWave / 16) {
+            const int row = r0 + pr / hn, h = h_lo + pr % hn;
             const float* tokp = qkv + ((size_t)row * tok_n + t) * stride + h * dh;
             float sc = 0.f;
             for (int e = 4 * pj; e < dh; e += 64) {
@@ -142,7 +151,7 @@ __global__ __launch_bounds__(kWave) void group_attention_f32(const GroupArgs a, 
         // from memory: a load here would stall every group change on its latency.
         jb.ge = jb.valid ? min(max(__builtin_amdgcn_readlane(ge_l, b), jb.gs + 1), rows) : jb.gs + 1;
         jb.qc = 0;
-        jb.h = 0;
+        jb.h = h_lo;
         jb.kt = 0;
         jb.rest = jb.valid ? rest & (rest - 1) : 0;
         return jb;
@@ -152,8 +161,8 @@ __global__ __launch_bounds__(kWave) void group_attention_f32(const GroupArgs a, 
         const int tiles = (jb.ge - jb.gs + kRT - 1) / kRT;
         if (++jb.kt < tiles) return jb;
         jb.kt = 0;
-        if (++jb.h < heads) return jb;
-        jb.h = 0;
+        if (++jb.h < h_hi) return jb;
+        jb.h = h_lo;
         if (++jb.qc * kQT < tiles) return jb;
         return first_of(jb.rest);
     };
@@ -319,10 +328,23 @@ __global__ __launch_bounds__(kWave) void group_attention_f32(const GroupArgs a, 
 
 }  // namespace
 
+// Waves per (16-row tile, slot), each taking a range of the heads. A tile's work is that of the
+// groups starting in it, so with one wave per tile the tiles where long groups start run several
+// times the mean while covered tiles return at once, and the last waves of a launch set its end.
+// Splitting the heads over 4 waves moves no extra bytes (heads own disjoint q, k and v).
+// JITCAST_HIP_GROUP_SPLIT (1..16) overrides it; read at every launch.
+static int group_head_split() {
+    const char* e = getenv("JITCAST_HIP_GROUP_SPLIT");
+    const int v = e ? atoi(e) : 0;
+    return v >= 1 && v <= 16 ? v : 4;
+}
+
 template <int DHP, bool TS, bool EXACT, bool X3 = false>
 static hipError_t launch_group(GroupArgs a, int dh, hipStream_t stream) {
     a.rtiles = (a.rows + kRT - 1) / kRT;
-    const uint64_t grid = (uint64_t)a.rtiles * a.n;
+    a.hsplit = std::min(group_head_split(), a.heads);
+    const uint64_t grid = (uint64_t)a.rtiles * a.n * a.hsplit;
+    if (grid > 0xffffffffull) return hipErrorInvalidValue;
     hipLaunchKernelGGL((group_attention_f32<DHP, TS, EXACT, X3>), dim3((uint32_t)grid), dim3(kWave), 0, stream, a,
                        dh);
     return hipGetLastError();

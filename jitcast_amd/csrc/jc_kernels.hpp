@@ -41,6 +41,7 @@ struct GroupArgs {
     int covariates;         // Timestral: whether the block runs the covariate rules
     float qscale;           // score scale times log2(e), folded into q
     int rtiles;             // 16-row tiles, set by the launcher
+    int hsplit;             // head ranges per (tile, slot), one wave each; set by the launcher
 };
 
 // Chronos-2 group attention (ts = false) or Timestral variate attention (ts = true); a.rtiles is
