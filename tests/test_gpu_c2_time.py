@@ -219,6 +219,35 @@ def test_fp32_folded_last_query(gpu, oracle, n, kind):
     assert np.isnan(got[:, :, heads * dh:]).all(), "columns past heads * dh are not written"
 
 
+@pytest.mark.parametrize("n,kind,table", [(130, "pad", True), (133, "random", True), (136, "all", True),
+                                          (261, "pad", True), (133, "pad", False), (137, "pad", True)])
+def test_fp32_tail_queries(gpu, oracle, n, kind, table):
+    """Rows of 128k + R tokens (the forecasts' 128 patches + [REG] + 4 future patches give R = 5):
+    the R tail queries run in a workgroup of their own. Against the oracle, the tail rows checked on
+    their own per head."""
+    rows, heads, dh, inner = 3, 3, 64, 200
+    print(f"case tail queries n={n} {kind} table={table}", flush=True)
+    qkv = cases.qkv(43, rows * n, inner)
+    live = _live(kind, 43, rows, n)
+    got = _run(qkv, live, rows, n, heads, dh, inner, table=table).reshape(rows, n, inner)
+    if table:
+        exp = oracle.c2_time_attention(qkv, live, rows, n, heads, dh, inner).reshape(rows, n, inner)
+    else:  # qkv taken as already rotated: plain attention over the live keys, in float64
+        q, k, v = brute.split_qkv(qkv, rows, n, heads, dh, inner)
+        sc = np.einsum("rqhe,rkhe->rhqk", q.astype(np.float64), k.astype(np.float64))
+        sc = np.where(live[:, None, None, :] == 1, sc, -np.inf)
+        pr = np.exp(sc - sc.max(-1, keepdims=True))
+        o = np.einsum("rhqk,rkhe->rqhe", pr / pr.sum(-1, keepdims=True), v.astype(np.float64))
+        exp = np.full((rows, n, inner), np.nan)
+        exp[:, :, : heads * dh] = o.reshape(rows, n, heads * dh)
+    assert oracle.rel_max_error(got[:, :, : heads * dh], exp[:, :, : heads * dh]) <= TOL_F32
+    tail = n % 128
+    for h in range(heads):
+        sl = np.s_[:, n - tail:, h * dh:(h + 1) * dh]
+        assert oracle.rel_max_error(got[sl], exp[sl]) <= TOL_F32, h
+    assert np.isnan(got[:, :, heads * dh:]).all(), "columns past heads * dh are not written"
+
+
 @pytest.mark.parametrize("n", [33, 161, 513])
 @pytest.mark.parametrize("pattern", ["last dead", "only last", "all", "pad"])
 def test_fp32_last_key(gpu, oracle, n, pattern):
