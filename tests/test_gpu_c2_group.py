@@ -33,6 +33,8 @@ CASES = [
     (17, 1, 1, 64, 64, 17, 17, 1.0),
     (48, 5, 12, 64, 768, 1, 1, 0.7),  # one-row groups: the streaming path
     (21, 3, 2, 16, 32, 1, 1, 0.5),
+    (260, 3, 12, 64, 768, 260, 260, 0.9),  # one group of a whole batch (cross-learning): 5 query chunks
+    (40, 2, 5, 64, 320, 1, 30, 0.8),  # 5 heads over 4 waves per tile: ranges of 1 and 2 heads
 ]
 
 

@@ -129,3 +129,41 @@ def test_config0_fixture_through_the_engine(gpu, oracle, tmp_path):
         errs = [oracle.rel_max_error(seen[f"layer{i}"], g["layers"][i]) for i in range(c.num_layers)]
         print("config 0 layers rel err " + " ".join(f"{e:.1e}" for e in errs), flush=True)
         assert max(errs) <= 1e-4
+
+
+@pytest.mark.parametrize("cross,max_tokens", [(True, 131072), (False, 500)])
+def test_engine_cross_learning_and_token_splits(gpu, oracle, checkpoint, cross, max_tokens):
+    """Through the engine, against the restatement over the oracle's forward: cross-learning (one
+    group per batch, so the group attention runs over every row of the batch), and a token budget
+    that splits each pass into several by whole groups. fp32: every call within 1e-4, forecasts
+    within 1e-3."""
+    from jitcast_amd.pipeline import Options
+
+    print(f"case engine cross={cross} max_tokens={max_tokens}", flush=True)
+    horizon = 40
+    series = _mixed_batch(17, 30, horizon)
+    _, w = ck.load_chronos2(checkpoint)
+    calls = []
+    with HipChronos2Engine.load(checkpoint, dtype="f32") as eng:
+        fwd = eng.forward_pass()
+        ofwd = _oracle_forward(oracle, C, w)
+
+        def checked(inp):
+            out = fwd(inp)
+            err = oracle.rel_max_error(out, ofwd(inp.context, inp.group, inp.future_covariates, inp.output_patches))
+            calls.append((inp.rows(), len(np.unique(inp.group)), err))
+            print(f"  call{len(calls) - 1} rows={inp.rows()} groups={calls[-1][1]} rel err {err:.2e}", flush=True)
+            return out
+
+        pipe = eng.pipeline().with_options(Options.defaults(C).with_cross_learning(cross)).with_max_tokens(max_tokens)
+        pipe.forward = checked
+        got = pipe.forecast([TimeSeries(t, p, k) for t, p, k in series], horizon)
+    exp = ref.forecast(C, _oracle_forward(oracle, C, w), series, horizon, cross_learning=cross, max_tokens=max_tokens)
+    assert calls and max(e for _, _, e in calls) <= 1e-4
+    if cross:
+        assert all(g == 1 for _, g, _ in calls), "one group per batch"
+    else:
+        assert len(calls) > 1, "the budget splits the pass"
+    err = max(oracle.rel_max_error(g.values, e) for g, e in zip(got, exp))
+    print(f"  forecasts rel err {err:.2e} (bar 1e-3)", flush=True)
+    assert err <= 1e-3
