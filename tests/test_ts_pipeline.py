@@ -127,6 +127,27 @@ def test_native_statistics_equal_the_scalar_loops():
             np.testing.assert_array_equal(scales[i], want[1])
 
 
+def test_native_statistics_reject_bad_shapes():
+    """The host helpers return JC_EINVAL (raised as JitcastArgumentError) instead of reading past
+    their arguments: a context shorter than one patch or not a whole number of patches, a patch below
+    1, and a mask that does not match the values."""
+    from jitcast_amd._lib import JitcastArgumentError
+
+    x = np.ones((2, 12), np.float32)
+    obs = np.ones((2, 12), bool)
+    sinh = np.zeros((2, 1, 8))
+    with pytest.raises(JitcastArgumentError):
+        tp.advancing_frames(x[:, :4], obs[:, :4], sinh, 8, 1e-6)  # t < patch
+    with pytest.raises(JitcastArgumentError):
+        tp.advancing_frames(x, obs, sinh, 8, 1e-6)  # 12 steps is not a whole number of 8-step patches
+    with pytest.raises(JitcastArgumentError):
+        tp.advancing_frames(x[:, :8], obs[:, :8], np.zeros((2, 1, 0)), 0, 1e-6)  # patch 0
+    with pytest.raises(ValueError):
+        tp.context_stats(x, obs[:, :6], 1e-6)
+    loc, scale, lo, hi = tp.context_stats(np.zeros((0, 5), np.float32), np.zeros((0, 5), bool), 1e-6)
+    assert loc.shape == scale.shape == lo.shape == hi.shape == (0,)
+
+
 def test_forward_fill_and_clamp_non_finite():
     x = np.array([0, 0, 3, 0, 5, 0], np.float32)
     m = np.array([False, False, True, False, True, False])
