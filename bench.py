@@ -136,7 +136,7 @@ def group_attention_line(steps: int, warmup: int, cpu: bool = True) -> dict:
     log(f"group attention: {ms:.4f} ms, {gbs:.0f} GB/s algorithmic ({100 * gbs / PEAK_HBM_GBS:.1f}% of HBM)")
     res = {
         "workload": "config 2: fp32 Chronos-2 group attention, 4096 rows x 129 slots, 12x64, groups U{1..64}",
-        "kernel": "jc::group_attention_f32<64, false, true>",
+        "kernel": "jc::group_attention_f32<64, false, true, false>",
         "launch_ms": round(ms, 5),
         "value": round(gbs, 1),
         "unit": "GB/s",
@@ -781,7 +781,7 @@ def main() -> int:
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_FP32_TFLOPS, 4),
             "traffic": traffic_from_profile("c2_time_attention_f32_config1"),
-            "kernel": "jc::time_attention_f32<64, 32, true, false, true>",
+            "kernel": "jc::time_attention_f32<64, 32, true, false, true, true, false>",
             "launch_ms": round(launch_ms, 5),
         },
         "cpu_baseline": cpu,
