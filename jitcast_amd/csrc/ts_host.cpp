@@ -8,9 +8,11 @@
 // The arithmetic is the reference's double arithmetic in its order, with no contraction into FMAs
 // (the pragma below), and max / min propagate NaN as the pipeline's array code does, so the results
 // are bit-identical to it.
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <limits>
+#include <thread>
 #include <vector>
 
 #include "../../include/jitcast_hip.h"
@@ -43,6 +45,30 @@ inline Welford combine(const Welford& a, const Welford& b) {
     return {w, mean, m2};
 }
 
+// fn(r0, r1) over [0, rows) in contiguous ranges, on up to 16 host threads when there are at least
+// 2^18 values to go through (rows are independent, so each row's arithmetic is unchanged)
+template <class F>
+void for_rows(int rows, int64_t per_row, F fn) {
+    const int64_t total = (int64_t)rows * per_row;
+    const int hw = (int)std::max(1u, std::thread::hardware_concurrency());
+    const int nt = total < (1 << 18) ? 1 : std::min({rows, hw, 16});
+    if (nt <= 1) {
+        fn(0, rows);
+        return;
+    }
+    std::vector<std::thread> pool;
+    int started = 1;  // ranges 1..started-1 run on their own threads
+    try {
+        pool.reserve(nt - 1);
+        for (; started < nt; started++)
+            pool.emplace_back(fn, (int)((int64_t)rows * started / nt), (int)((int64_t)rows * (started + 1) / nt));
+    } catch (...) {  // no more threads: the remaining ranges run on this one
+    }
+    fn(0, (int)((int64_t)rows / nt));
+    for (int i = started; i < nt; i++) fn((int)((int64_t)rows * i / nt), (int)((int64_t)rows * (i + 1) / nt));
+    for (auto& th : pool) th.join();
+}
+
 }  // namespace
 
 extern "C" {
@@ -53,7 +79,9 @@ int jc_ts_context_stats(const float* x, const uint8_t* observed, int rows, int t
     if (rows < 0 || t < 0 || (rows > 0 && t > 0 && (!x || !observed)))
         return jc::host_fail(JC_EINVAL, "jc_ts_context_stats: bad arguments (rows=%d t=%d)", rows, t);
     const double min_s = (double)minimum_scale;
-    for (int r = 0; r < rows; r++) {
+    for_rows(rows, t, [&](int ra, int rb) {
+#pragma clang fp contract(off)
+    for (int r = ra; r < rb; r++) {
         const float* xr = x + (size_t)r * t;
         const uint8_t* mr = observed + (size_t)r * t;
         double cum_w = 0.0, cum_x = 0.0, m2 = 0.0, prev = 0.0, mean = 0.0;
@@ -78,6 +106,7 @@ int jc_ts_context_stats(const float* x, const uint8_t* observed, int rows, int t
         if (hi) hi[r] = mx == -std::numeric_limits<float>::infinity() ? 0.0f : mx;
         if (lo) lo[r] = mn == std::numeric_limits<float>::infinity() ? 0.0f : mn;
     }
+    });
     return JC_OK;
 }
 
@@ -92,9 +121,11 @@ int jc_ts_advancing_frames(const float* context, const uint8_t* observed, const 
     const int n = n_ctx + n_pred;
     const double clip = std::sqrt((double)std::numeric_limits<float>::max()) / 1e3;
     const double min_s = (double)minimum_scale;
+    for_rows(rows, t, [&](int ra, int rb) {
+#pragma clang fp contract(off)
     std::vector<Welford> st(n);
     std::vector<double> folded(patch);
-    for (int r = 0; r < rows; r++) {
+    for (int r = ra; r < rb; r++) {
         const float* cr = context + (size_t)r * t;
         const uint8_t* mr = observed + (size_t)r * t;
         // each context patch's (count, mean, m2), summed in order within the patch
@@ -142,6 +173,7 @@ int jc_ts_advancing_frames(const float* context, const uint8_t* observed, const 
             c = combine(c, Welford{(double)patch, b_mean, b_m2});
         }
     }
+    });
     return JC_OK;
 }
 

@@ -127,6 +127,24 @@ def test_native_statistics_equal_the_scalar_loops():
             np.testing.assert_array_equal(scales[i], want[1])
 
 
+def test_native_statistics_threaded_equal_row_by_row():
+    """Past 2^18 values the helpers split the rows over host threads: the same bits as each row
+    computed alone (a single-threaded call)."""
+    r = np.random.default_rng(9)
+    rows, t, ps, hp = 64, 8192, 16, 4
+    x = (r.standard_normal((rows, t)) * 5 + 2).astype(np.float32)
+    obs = r.random((rows, t)) > 0.2
+    sinh = r.standard_normal((rows, hp, ps))
+    many = tp.context_stats(x, obs, 1e-6)
+    frames = tp.advancing_frames(x, obs, sinh, ps, 1e-6)
+    for i in range(0, rows, 7):
+        one = tp.context_stats(x[i:i + 1], obs[i:i + 1], 1e-6)
+        for a, b in zip(many, one):
+            assert a[i].tobytes() == b[0].tobytes()
+        f1 = tp.advancing_frames(x[i:i + 1], obs[i:i + 1], sinh[i:i + 1], ps, 1e-6)
+        assert frames[0][i].tobytes() == f1[0][0].tobytes() and frames[1][i].tobytes() == f1[1][0].tobytes()
+
+
 def test_native_statistics_reject_bad_shapes():
     """The host helpers return JC_EINVAL (raised as JitcastArgumentError) instead of reading past
     their arguments: a context shorter than one patch or not a whole number of patches, a patch below
