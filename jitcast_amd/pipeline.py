@@ -154,19 +154,19 @@ class Chronos2Pipeline:
     def _predict_batch(self, batch: list, horizon: int) -> list:
         c = self.config
         length = max(p.context[0].size for p in batch)
-        n_rows = sum(len(p.context) for p in batch)
-        context = np.full((n_rows, length), np.nan, F32)
-        future = np.empty((n_rows, horizon), F32)
-        group = np.empty(n_rows, np.int32)
-        first_row = []
-        r = 0
-        for s, p in enumerate(batch):
-            first_row.append(r)
-            for i, row in enumerate(p.context):
+        counts = np.array([len(p.context) for p in batch], np.int64)
+        n_rows = int(counts.sum())
+        first_row = (np.cumsum(counts) - counts).tolist()
+        all_rows = [row for p in batch for row in p.context]
+        if all(row.size == length for row in all_rows):  # no left padding: one copy
+            context = np.stack(all_rows).astype(F32, copy=False)
+        else:
+            context = np.full((n_rows, length), np.nan, F32)
+            for r, row in enumerate(all_rows):
                 context[r, length - row.size:] = row
-                future[r] = p.future[i]
-                group[r] = 0 if self.options.cross_learning else s
-                r += 1
+        future = np.concatenate([p.future for p in batch]).astype(F32, copy=False)
+        ids = np.zeros(len(batch), np.int32) if self.options.cross_learning else np.arange(len(batch), dtype=np.int32)
+        group = np.repeat(ids, counts)
         rows, q = n_rows, c.num_quantiles
         prediction = self._predict_step(context, group, future, self._output_patches(horizon))
         predictions = [prediction]
