@@ -678,13 +678,13 @@ def main() -> int:
             print(json.dumps({"also": also}), flush=True)
             return 0
     if args.only in ("all", "ts-forecast"):
-        for name in ("bf16", "f32"):
+        for name in ("bf16", "f16x3", "f32"):
             also[f"ts_forecast_{name}"] = ts_forecast_line(name)
         if args.only == "ts-forecast":
             print(json.dumps({"also": also}), flush=True)
             return 0
     if args.only in ("all", "ts-block", "ts-block-bf16"):
-        for name in (("bf16",) if args.only == "ts-block-bf16" else ("bf16", "f32")):
+        for name in (("bf16",) if args.only == "ts-block-bf16" else ("bf16", "f16x3", "f32")):
             also[f"ts_block_{name}"] = ts_block_line(2, 1, name)
         if args.only in ("ts-block", "ts-block-bf16"):
             print(json.dumps({"also": also}), flush=True)

@@ -123,9 +123,9 @@ class HipTimestralEngine(ForecastEngine):
         from .timestral_model import HipTimestralModel
         from .ts_pipeline import DEFAULT_BATCH_SIZE, TimestralPipeline
 
-        dtype = dtype if dtype is not None else opts.choice("timestral.hip.dtype", "f32", "f32", "bf16", "fp16")
-        if dtype not in ("f32", "bf16", "fp16"):
-            raise ValueError(f"dtype must be f32, bf16 or fp16, got {dtype}")
+        dtype = dtype if dtype is not None else opts.choice("timestral.hip.dtype", "f32", "f32", "bf16", "fp16", "f16x3")
+        if dtype not in ("f32", "bf16", "fp16", "f16x3"):
+            raise ValueError(f"dtype must be f32, bf16, fp16 or f16x3, got {dtype}")
         device = device if device is not None else opts.integer("jitcast.hip.device", 0, 0)
         self._config = config
         self._dtype = dtype

@@ -13,7 +13,8 @@ Properties read by this package:
   chronos2.hip.planBytes    device bytes the cached plans may hold (the device's memory)
   timestral.maxTokens       tokens (rows x patches) per Timestral forward pass before the pipeline
                             splits a call into windows (131072)
-  timestral.hip.dtype       f32 | bf16 | fp16: the Timestral engine's GEMM and attention type (f32)
+  timestral.hip.dtype       f32 | bf16 | fp16 | f16x3: the Timestral engine's GEMM and attention type (f32;
+                            f16x3: fp32 activations, each GEMM over three-term fp16 splits)
   timestral.hip.buckets     pad blocks to shared shapes before the forward (true)
   timestral.hip.plans       plans cached per HipTimestralModel, one hipGraph per block shape; 0 runs
                             eagerly (8)

@@ -124,7 +124,10 @@ class HipTimestralModel:
     "fp16" mirror its FP16 GEMM mode (TimestralForward.java:467-499 with Kernels.gemmHalf): the
     attention sublayers' and the MLP's GEMMs take storage-type operands with fp32 accumulation, the
     time attention and SwiGLU run in the storage type, the variate attention reads fp32 q|k|v, the
-    residual stream, norms' inputs, the embedding and the head stay fp32."""
+    residual stream, norms' inputs, the embedding and the head stay fp32. "f16x3" (no reference
+    counterpart) keeps every activation fp32 and runs each of those GEMMs on fp16 MFMA over
+    three-term splits of its operands (weights split once at load, [hi | lo | hi]; the A operand
+    split after its norm, attention or SwiGLU, [hi | hi | lo]): about fp32's accuracy."""
 
     def __init__(self, c: TimestralConfig, weights: dict, dtype: str = "f32", device: int = 0,
                  max_plans: int | None = None, plan_bytes: int | None = None, buckets: bool | None = None):
@@ -138,8 +141,8 @@ class HipTimestralModel:
         import torch
 
         self.c, self.dtype = c, dtype
-        self.code = {"f32": _lib.JC_F32, "bf16": _lib.JC_BF16, "fp16": _lib.JC_F16}[dtype]
-        self.tdt = {"f32": torch.float32, "bf16": torch.bfloat16, "fp16": torch.float16}[dtype]
+        self.code = {"f32": _lib.JC_F32, "bf16": _lib.JC_BF16, "fp16": _lib.JC_F16, "f16x3": _lib.JC_F16X3}[dtype]
+        self.tdt = {"f32": torch.float32, "bf16": torch.bfloat16, "fp16": torch.float16, "f16x3": torch.float16}[dtype]
         self.dev = torch.device("cuda", device)
         t = lambda a: None if a is None else torch.from_numpy(np.ascontiguousarray(a)).to(self.dev)  # noqa: E731
 
@@ -147,6 +150,10 @@ class HipTimestralModel:
             if a is None or self.code == _lib.JC_F32:
                 return t(a)
             src = t(a)
+            if self.code == _lib.JC_F16X3:  # its three-term fp16 split [hi | lo | hi], [n, 3k]
+                dst = torch.empty(src.shape[0], 3 * src.shape[1], dtype=torch.float16, device=self.dev)
+                chronos2.split_f16x3(src, dst, weights=True)
+                return dst
             dst = torch.empty(src.shape, dtype=self.tdt, device=self.dev)
             chronos2.to_lp(src, dst)
             return dst
@@ -184,7 +191,9 @@ class HipTimestralModel:
             "raw": e(rows * h, c.patch_size * c.num_quantiles),
             "table": torch.from_numpy(timestral.rope_table(enc, n, c.head_dim, c.rope_dim, c.rope_theta)).to(self.dev),
         }
-        if self.code != _lib.JC_F32:
+        if self.code == _lib.JC_F16X3:  # the split of each GEMM's A operand, [tokens, 3k] fp16
+            b["x3"] = torch.empty(tokens * 3 * max(d, f), dtype=torch.float16, device=self.dev)
+        elif self.code != _lib.JC_F32:
             s = lambda *sh: torch.empty(*sh, dtype=self.tdt, device=self.dev)  # noqa: E731
             b.update({"hn_lp": s(tokens, d), "big_lp": s(tokens, max(3 * d, 2 * f)), "att_lp": s(tokens, d),
                       "gate_lp": s(tokens, d), "act_lp": s(tokens, f)})
@@ -245,20 +254,28 @@ class HipTimestralModel:
         b = bufs if bufs is not None else self._buffers(rows, enc, h)
         ctx = chronos2.context(self.dev.index or 0)
         p = chronos2._ptr
-        lowp = self.code != _lib.JC_F32
+        x3 = self.code == _lib.JC_F16X3  # fp32 activations, each GEMM over three-term fp16 splits
+        lowp = self.code != _lib.JC_F32 and not x3  # storage-type operands (the FP16 GEMM mode)
 
         def view(buf, width):  # a contiguous [tokens, width] view of a shared buffer
             return buf.view(-1)[: tokens_n * width].view(tokens_n, width)
+
+        def operand(src, k):  # a GEMM's A operand: src itself, or (f16x3) its split [hi | hi | lo]
+            if not x3:
+                return src
+            dst = view(b["x3"], 3 * k)
+            chronos2.split_f16x3(src, dst)
+            return dst
 
         def norm(wt):  # the pre-norm, in the GEMM operands' type
             if lowp:
                 chronos2.rms_norm_lp(x, wt, b["hn_lp"], c.norm_eps)
                 return b["hn_lp"]
             chronos2.rms_norm(x, wt, b["hn"], c.norm_eps)
-            return b["hn"]
+            return operand(b["hn"], d)
 
         def gemm(a, wt, out, flags=0):
-            (chronos2.linear_lp if lowp else chronos2.linear)(a, wt, out, flags=flags)
+            (chronos2.linear_lp if lowp or x3 else chronos2.linear)(a, wt, out, flags=flags)
 
         for lw in self.layers:
             for a in lw["attentions"]:
@@ -281,15 +298,15 @@ class HipTimestralModel:
                 if lowp and not a["time"]:
                     chronos2.to_lp(att, b["att_lp"])
                     att = b["att_lp"]
-                gemm(att, a["wo"], x, chronos2.GEMM_ACCUMULATE)
+                gemm(operand(att, d), a["wo"], x, chronos2.GEMM_ACCUMULATE)
             if not mlp:
                 continue
             hn = norm(lw["mlp_norm"])
             up = view(b["big_lp"] if lowp else b["big"], 2 * f)
             act = b["act_lp"] if lowp else b["act"]
             gemm(hn, lw["up"], up)
-            _lib.call("jc_swiglu", ctx.handle, p(up), p(act), tokens_n, f, self.code)
-            gemm(act, lw["down"], x, chronos2.GEMM_ACCUMULATE)
+            _lib.call("jc_swiglu", ctx.handle, p(up), p(act), tokens_n, f, self.code if lowp else _lib.JC_F32)
+            gemm(operand(act, f), lw["down"], x, chronos2.GEMM_ACCUMULATE)
 
     def predict_block(self, inputs, observed, group, h: int, role=None, known_future=None, known_future_mask=None):
         """TimestralForward.predictBlock (TimestralForward.java:186-195): with buckets on, the block padded

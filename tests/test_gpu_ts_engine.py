@@ -151,7 +151,7 @@ def long_checkpoint(tmp_path_factory):
     return d
 
 
-@pytest.mark.parametrize("dtype,bar", [("f32", 1e-4), ("bf16", 5e-2), ("fp16", 5e-2)])
+@pytest.mark.parametrize("dtype,bar", [("f32", 1e-4), ("f16x3", 1e-4), ("bf16", 5e-2), ("fp16", 5e-2)])
 def test_mixed_batch_calls_match_the_oracle_forward(gpu, oracle, long_checkpoint, dtype, bar):
     """TimestralBatchParityAccelTest.mixedBatchMatchesTheCpuReference: 37 mixed series at horizon 1100
     (several blocks per pass, both sign passes), every predict_block call of the engine's pipeline

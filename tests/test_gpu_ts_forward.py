@@ -186,11 +186,12 @@ def test_predict_block_matches_oracle(gpu, oracle, covariates):
     assert np.all(np.diff(got, axis=2) >= 0)  # non-crossing
 
 
-@pytest.mark.parametrize("dt", ["bf16", "fp16"])
+@pytest.mark.parametrize("dt,bar", [("bf16", 2e-2), ("fp16", 2e-2), ("f16x3", 1e-4)])
 @pytest.mark.parametrize("name,c,rows,groups,enc,h,covariates", [CASES[0], CASES[2]], ids=["tiny", "d128"])
-def test_forward_lowp_matches_fp32_oracle(gpu, oracle, dt, name, c, rows, groups, enc, h, covariates):
+def test_forward_lowp_matches_fp32_oracle(gpu, oracle, dt, bar, name, c, rows, groups, enc, h, covariates):
     """The FP16-GEMM mode (storage-type GEMM operands and time attention, fp32 accumulation and
-    residual stream) against the fp32 oracle on the same unrounded weights: within 2e-2."""
+    residual stream) against the fp32 oracle on the same unrounded weights: within 2e-2. f16x3 (fp32
+    activations, every GEMM over three-term fp16 splits): within fp32's bar, 1e-4."""
     print(f"case ts forward {dt} {name}", flush=True)
     ll = enc - h if covariates else enc
     kv, known, position = cases.ts_layout(17, rows, enc, ll, h, known_frac=0.3 if covariates else 0.0)
@@ -210,4 +211,4 @@ def test_forward_lowp_matches_fp32_oracle(gpu, oracle, dt, name, c, rows, groups
                                 c.head_dim, c.rope_dim, c.norm_eps, c.rope_theta)
     err = oracle.rel_max_error(raw.cpu().numpy(), exp)
     print(f"  raw rel err {err:.3e}", flush=True)
-    assert err <= 2e-2
+    assert err <= bar
