@@ -406,7 +406,9 @@ int jc_linear_lp(jc_ctx *ctx, const void *a, int lda, const void *w, const float
                  int n, int k, int flags, int dtype, int c_dtype);
 
 /* Kernels.rmsNorm with its twin output (J/tornado/Kernels.java:800-829): y in the storage type
- * `dtype` = x * (1 / sqrt(mean(x^2) + eps)) * w, x fp32; d a multiple of 4; 16-byte aligned. */
+ * `dtype` = x * (1 / sqrt(mean(x^2) + eps)) * w, x fp32; d a multiple of 4; 16-byte aligned.
+ * dtype JC_F16X3 (no reference counterpart): y is fp16 [rows, 3d], the fp32 result's A-operand
+ * split [hi | hi | lo] (jc_split_f16x3's layout), ready for a JC_F16X3 GEMM. */
 int jc_rms_norm_lp(jc_ctx *ctx, const float *x, const float *w, void *y, int rows, int d, float eps, int dtype);
 
 /* dst[i] = src[i] rounded to the storage type `dtype`, saturated to its finite range (Kernels.toHalf,

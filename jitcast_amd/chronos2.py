@@ -215,6 +215,17 @@ def rms_norm_lp(x, w, y, eps: float) -> None:
     _lib.call("jc_rms_norm_lp", ctx.handle, _ptr(x), _ptr(w), _ptr(y), rows, d, ctypes.c_float(eps), _dtype_code(y))
 
 
+def rms_norm_x3(x, w, y3, eps: float) -> None:
+    """y3 float16 [rows, 3d] = the split [hi | hi | lo] of rmsNorm(x), x float32 [rows, d]
+    (jc_rms_norm_lp with JC_F16X3): the norm and jc_split_f16x3 in one pass."""
+    _f32(x, "x")
+    rows, d = x.shape
+    if y3.dim() != 2 or tuple(y3.shape) != (rows, 3 * d) or _dtype_code(y3) != _lib.JC_F16:
+        raise _lib.JitcastArgumentError(_lib.JC_EINVAL, "rms_norm_x3: y3 must be float16 [rows, 3d]")
+    ctx = context(x.device.index or 0)
+    _lib.call("jc_rms_norm_lp", ctx.handle, _ptr(x), _ptr(w), _ptr(y3), rows, d, ctypes.c_float(eps), _lib.JC_F16X3)
+
+
 def split_f16x3(src, dst, weights: bool = False) -> None:
     """dst float16 [rows, 3k] = the three-term split of src float32 [rows, k] (jc_split_f16x3):
     [hi | hi | lo] per row, or [hi | lo | hi] with weights, hi = fp16(v) saturated, lo = fp16(v - hi)."""

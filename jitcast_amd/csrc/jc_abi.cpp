@@ -860,14 +860,15 @@ int jc_linear_lp(jc_ctx* ctx, const void* a, int lda, const void* w, const float
 
 static int launch_rms_lp(jc_ctx* ctx, const char* W, const float* x, const float* w, void* y, int rows, int d, float eps,
                          int dtype) {
-    int rc = check_lp_dtype(W, dtype);
+    int rc = dtype == JC_F16X3 ? JC_OK : check_lp_dtype(W, dtype);
     if (rc) return rc;
     if (rows < 0 || d < 0) return fail(JC_EINVAL, "%s: negative size", W);
     if ((size_t)rows * d == 0) return JC_OK;
     if (!x || !y) return fail(JC_EINVAL, "%s: null x or y", W);
     if (d % 4) return fail(JC_EINVAL, "%s: d must be a multiple of 4 (got %d)", W, d);
     if (!aligned16(x) || !aligned16(y) || (w && !aligned16(w))) return fail(JC_EINVAL, "%s: 16-byte alignment", W);
-    hipError_t e = jc::rms_norm_lp_launch(x, y, w, rows, d, eps, dtype == JC_F16, ctx->stream);
+    hipError_t e = dtype == JC_F16X3 ? jc::rms_norm_x3_launch(x, y, w, rows, d, eps, ctx->stream)
+                                     : jc::rms_norm_lp_launch(x, y, w, rows, d, eps, dtype == JC_F16, ctx->stream);
     return e == hipSuccess ? JC_OK : hip_fail(W, e);
 }
 

@@ -271,8 +271,12 @@ class HipTimestralModel:
             if lowp:
                 chronos2.rms_norm_lp(x, wt, b["hn_lp"], c.norm_eps)
                 return b["hn_lp"]
+            if x3:  # the norm writes the split itself
+                y3 = view(b["x3"], 3 * d)
+                chronos2.rms_norm_x3(x, wt, y3, c.norm_eps)
+                return y3
             chronos2.rms_norm(x, wt, b["hn"], c.norm_eps)
-            return operand(b["hn"], d)
+            return b["hn"]
 
         def gemm(a, wt, out, flags=0):
             (chronos2.linear_lp if lowp or x3 else chronos2.linear)(a, wt, out, flags=flags)

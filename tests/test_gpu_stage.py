@@ -188,6 +188,28 @@ def test_split_f16x3_is_exact(gpu, weights):
     assert np.all(np.abs(recon[ok] - v[ok]) <= 2 ** -22 * np.abs(v[ok]) + 2 ** -25)
 
 
+def test_rms_norm_x3_is_the_split_of_the_norm(gpu):
+    """jc_rms_norm_lp with JC_F16X3 writes the A-operand split [hi | hi | lo] of rmsNorm(x): both hi
+    copies equal, and hi + lo within 2^-21 of jc_rms_norm's fp32 result plus fp16's subnormal
+    spacing (the split's 2^-22 and an ulp of the norm's own rounding)."""
+    rows, d = 45, 136
+    r = np.random.default_rng(3)
+    x = _t((r.standard_normal((rows, d)) * 3).astype(np.float32))
+    w = _t((1 + 0.1 * r.standard_normal(d)).astype(np.float32))
+    y3 = torch.empty(rows, 3 * d, dtype=torch.float16, device=DEV)
+    y = torch.empty(rows, d, device=DEV)
+    chronos2.rms_norm_x3(x, w, y3, 1e-6)
+    chronos2.rms_norm(x, w, y, 1e-6)
+    torch.cuda.synchronize()
+    got = y3.cpu().numpy()
+    ref = y.cpu().numpy().astype(np.float64)
+    np.testing.assert_array_equal(got[:, :d].view(np.uint16), got[:, d:2 * d].view(np.uint16))
+    recon = got[:, :d].astype(np.float64) + got[:, 2 * d:].astype(np.float64)
+    assert np.all(np.abs(recon - ref) <= 2 ** -21 * np.abs(ref) + 2 ** -24)
+    with pytest.raises(JitcastArgumentError):
+        chronos2.rms_norm_x3(x, w, torch.empty(rows, 2 * d, dtype=torch.float16, device=DEV), 1e-6)
+
+
 LP = {"bf16": torch.bfloat16, "fp16": torch.float16}
 
 
