@@ -496,6 +496,8 @@ int jc_ts_gather_decoder(jc_ctx *ctx, const float *y, float *dec, int rows, int 
  * act [tokens, f] = SiLU(up[t][j]) * up[t][f + j] with up [tokens, 2f], computed in fp32:
  * Kernels.swiGlu and, for dtype JC_BF16 / JC_F16, Kernels.swiGluHalf with the result saturated to the
  * type's finite range (J/tornado/Kernels.java:832-856). up and act are both of `dtype`.
+ * dtype JC_F16X3 (no reference counterpart): up fp32, act fp16 [tokens, 3f], the fp32 result's
+ * A-operand split [hi | hi | lo] for a JC_F16X3 GEMM; f a multiple of 4, 16-byte alignment.
  */
 int jc_swiglu(jc_ctx *ctx, const void *up, void *act, int64_t tokens, int f, int dtype);
 

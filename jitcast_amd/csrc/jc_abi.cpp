@@ -1146,10 +1146,13 @@ int jc_swiglu(jc_ctx* ctx, const void* up, void* act, int64_t tokens, int f, int
     const char* W = "jc_swiglu";
     int rc = use(ctx, W);
     if (rc) return rc;
-    if (dtype != JC_F32 && dtype != JC_BF16 && dtype != JC_F16) return fail(JC_EINVAL, "%s: unknown dtype %d", W, dtype);
+    if (dtype != JC_F32 && dtype != JC_BF16 && dtype != JC_F16 && dtype != JC_F16X3)
+        return fail(JC_EINVAL, "%s: unknown dtype %d", W, dtype);
     if (tokens < 0 || f < 0) return fail(JC_EINVAL, "%s: negative size (tokens=%lld f=%d)", W, (long long)tokens, f);
     if (tokens * (int64_t)f == 0) return JC_OK;
     if (!up || !act) return fail(JC_EINVAL, "%s: null up or act", W);
+    if (dtype == JC_F16X3 && (f % 4 || !aligned16(up) || !aligned16(act)))
+        return fail(JC_EINVAL, "%s: JC_F16X3 needs f a multiple of 4 (got %d) and 16-byte alignment", W, f);
     hipError_t e = jc::swiglu_launch(up, act, (uint64_t)tokens, f, dtype, ctx->stream);
     return e == hipSuccess ? JC_OK : hip_fail(W, e);
 }

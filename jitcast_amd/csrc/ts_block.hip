@@ -82,6 +82,33 @@ __global__ __launch_bounds__(256) void swiglu_vec(const T* __restrict__ up, T* _
     }
 }
 
+// JC_F16X3: SwiGLU's fp32 result (swiglu_vec<float>'s expression) written as the A-operand split
+// [hi | hi | lo] of the next GEMM, rows of 3f fp16, so no split pass follows. f a multiple of 4.
+__global__ __launch_bounds__(256) void swiglu_x3(const float* __restrict__ up, _Float16* __restrict__ act3,
+                                                 uint64_t tokens, int f) {
+    const uint64_t fv = (uint64_t)(f / 4);
+    const uint64_t total = tokens * fv;
+    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t id = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; id < total; id += stride) {
+        const uint64_t t = id / fv, j = (id - t * fv) * 4;
+        const float* gp = up + t * 2 * (uint64_t)f + j;
+        const floatx4 gv = *reinterpret_cast<const floatx4*>(gp);
+        const floatx4 uv = *reinterpret_cast<const floatx4*>(gp + f);
+        floatx4 o;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const float g = gv[k], u = uv[k];
+            o[k] = g / (1.f + expf(-g)) * u;
+        }
+        halfx4 hi, lo;
+        split_f16x4(o, hi, lo);
+        _Float16* row = act3 + t * 3 * (uint64_t)f;
+        *reinterpret_cast<halfx4*>(row + j) = hi;
+        *reinterpret_cast<halfx4*>(row + f + j) = hi;
+        *reinterpret_cast<halfx4*>(row + 2 * (uint64_t)f + j) = lo;
+    }
+}
+
 dim3 grid_for(uint64_t items) {
     const uint64_t blocks = (items + 255) / 256;
     return dim3((uint32_t)(blocks < 16384 ? (blocks ? blocks : 1) : 16384));
@@ -97,6 +124,11 @@ hipError_t ts_assemble_launch(const float* emb, const float* query, float* x, in
 }
 
 hipError_t swiglu_launch(const void* up, void* act, uint64_t tokens, int f, int dtype_code, hipStream_t stream) {
+    if (dtype_code == 3) {  // JC_F16X3: the caller checked f % 4 == 0 and the alignment
+        hipLaunchKernelGGL(swiglu_x3, grid_for(tokens * (uint64_t)(f / 4)), dim3(256), 0, stream, (const float*)up,
+                           (_Float16*)act, tokens, f);
+        return hipGetLastError();
+    }
     const int v = dtype_code == 0 ? 4 : 8;
     if (f % v == 0 && ((uintptr_t)up & 15u) == 0 && ((uintptr_t)act & 15u) == 0) {
         const dim3 g = grid_for(tokens * (uint64_t)(f / v));

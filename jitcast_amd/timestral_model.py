@@ -309,8 +309,12 @@ class HipTimestralModel:
             up = view(b["big_lp"] if lowp else b["big"], 2 * f)
             act = b["act_lp"] if lowp else b["act"]
             gemm(hn, lw["up"], up)
-            _lib.call("jc_swiglu", ctx.handle, p(up), p(act), tokens_n, f, self.code if lowp else _lib.JC_F32)
-            gemm(operand(act, f), lw["down"], x, chronos2.GEMM_ACCUMULATE)
+            if x3:  # SwiGLU writes the down projection's split operand itself
+                act = view(b["x3"], 3 * f)
+                _lib.call("jc_swiglu", ctx.handle, p(up), p(act), tokens_n, f, _lib.JC_F16X3)
+            else:
+                _lib.call("jc_swiglu", ctx.handle, p(up), p(act), tokens_n, f, self.code if lowp else _lib.JC_F32)
+            gemm(act, lw["down"], x, chronos2.GEMM_ACCUMULATE)
 
     def predict_block(self, inputs, observed, group, h: int, role=None, known_future=None, known_future_mask=None):
         """TimestralForward.predictBlock (TimestralForward.java:186-195): with buckets on, the block padded

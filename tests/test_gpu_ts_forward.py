@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 import torch
 
-from jitcast_amd import _lib, chronos2, timestral
+from jitcast_amd import JitcastArgumentError, _lib, chronos2, timestral
 from jitcast_amd import timestral_model as tm
 from tests import cases
 
@@ -26,6 +26,32 @@ def _i32(a):
 
 # f = 96: the 16-byte path for every type; 36: 16-byte for fp32, per element for bf16 / fp16; 35: per
 # element for every type
+@pytest.mark.parametrize("f", [96, 36])
+def test_swiglu_x3_is_the_split_of_the_fp32_swiglu(gpu, f):
+    """jc_swiglu with JC_F16X3 (fp32 up, fp16 act [tokens, 3f]) writes the A-operand split [hi | hi |
+    lo] of the fp32 SwiGLU: both hi copies equal, and hi + lo within 2^-21 of the fp32 jc_swiglu's
+    result plus fp16's subnormal spacing (the split's 2^-22 and an ulp of fp32 SwiGLU's own rounding,
+    which the two kernels may compile differently). f not a multiple of 4 is rejected."""
+    r = np.random.default_rng(8)
+    tokens = 301
+    ut = _t((3 * r.standard_normal((tokens, 2 * f))).astype(np.float32), torch.float32)
+    act = torch.empty(tokens, f, dtype=torch.float32, device=DEV)
+    act3 = torch.empty(tokens, 3 * f, dtype=torch.float16, device=DEV)
+    ctx = chronos2.context(0)
+    _lib.call("jc_swiglu", ctx.handle, chronos2._ptr(ut), chronos2._ptr(act), tokens, f, _lib.JC_F32)
+    _lib.call("jc_swiglu", ctx.handle, chronos2._ptr(ut), chronos2._ptr(act3), tokens, f, _lib.JC_F16X3)
+    torch.cuda.synchronize()
+    got = act3.cpu().numpy()
+    ref = act.cpu().numpy().astype(np.float64)
+    np.testing.assert_array_equal(got[:, :f].view(np.uint16), got[:, f:2 * f].view(np.uint16))
+    recon = got[:, :f].astype(np.float64) + got[:, 2 * f:].astype(np.float64)
+    err = np.abs(recon - ref)
+    print(f"  swiglu x3: max |hi + lo - fp32| / |fp32| {np.max(err / np.maximum(np.abs(ref), 1e-30)):.2e}", flush=True)
+    assert np.all(err <= 2 ** -21 * np.abs(ref) + 2 ** -24)
+    with pytest.raises(JitcastArgumentError):
+        _lib.call("jc_swiglu", ctx.handle, chronos2._ptr(ut), chronos2._ptr(act3), tokens, 35, _lib.JC_F16X3)
+
+
 @pytest.mark.parametrize("f", [96, 36, 35])
 @pytest.mark.parametrize("dt", ["f32", "bf16", "fp16"])
 def test_swiglu_matches_oracle(gpu, oracle, dt, f):
