@@ -177,7 +177,7 @@ def test_bf16_config1_shape_subset_matches_oracle(gpu, oracle, lp_kernel):
     assert err <= TOL_LP
 
 
-@pytest.mark.parametrize("n", [40, 129])
+@pytest.mark.parametrize("n", [40, 129, 133])
 def test_fp32_no_live_key_gives_zeros(gpu, oracle, n):
     rows, heads, dh, inner = 3, 2, 64, 128
     qkv = cases.qkv(29, rows * n, inner)
@@ -189,7 +189,7 @@ def test_fp32_no_live_key_gives_zeros(gpu, oracle, n):
     assert oracle.rel_max_error(got, exp) <= TOL_F32
 
 
-@pytest.mark.parametrize("n", [70, 129])
+@pytest.mark.parametrize("n", [70, 129, 133])
 def test_fp32_one_live_key_returns_its_value(gpu, n):
     rows, heads, dh, inner = 2, 2, 64, 128
     qkv = cases.qkv(31, rows * n, inner)
