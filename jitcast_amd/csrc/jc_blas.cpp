@@ -62,6 +62,7 @@ struct Blas {
     hipblasLtHandle_t handle = nullptr;
     void* ws = nullptr;
     size_t ws_bytes = 0;
+    size_t ws_limit = 0;  // the most workspace an algorithm may ask for (JITCAST_HIP_BLAS_WORKSPACE)
     float* zeros = nullptr;  // kZeroBias floats
     std::unordered_map<Key, Entry, KeyHash> cache;
     std::unordered_set<uint64_t> reported;  // declined shapes already reported (JITCAST_HIP_BLAS_DEBUG)
@@ -75,6 +76,11 @@ Blas* blas_create() {
         return nullptr;
     }
     b->ws_bytes = kBlasWorkspaceBytes;
+    b->ws_limit = b->ws_bytes;
+    if (const char* e = getenv("JITCAST_HIP_BLAS_WORKSPACE")) {
+        const unsigned long long v = strtoull(e, nullptr, 10);
+        b->ws_limit = v < b->ws_bytes ? (size_t)v : b->ws_bytes;
+    }
     if (hipMalloc(&b->ws, b->ws_bytes) != hipSuccess) {
         (void)hipblasLtDestroy(b->handle);
         delete b;
@@ -130,7 +136,7 @@ static Entry* entry_for(Blas* b, const Key& key) {
     if (good) {
         hipblasLtMatmulPreference_t pref = nullptr;
         if (hipblasLtMatmulPreferenceCreate(&pref) == 0) {
-            const uint64_t wsb = b->ws_bytes;
+            const uint64_t wsb = b->ws_limit;
             constexpr int kAsk = 8;
             hipblasLtMatmulHeuristicResult_t res[kAsk];
             int got = 0;
@@ -138,7 +144,7 @@ static Entry* entry_for(Blas* b, const Key& key) {
                                                       sizeof wsb) == 0 &&
                 hipblasLtMatmulAlgoGetHeuristic(b->handle, e.desc, e.lw, e.la, e.lc, e.lc, pref, kAsk, res, &got) == 0) {
                 for (int i = 0; i < got; i++) {  // the heuristic's order: the first that fits the workspace
-                    if (res[i].workspaceSize <= b->ws_bytes) {
+                    if (res[i].workspaceSize <= b->ws_limit) {
                         e.algo = res[i].algo;
                         e.ok = true;
                         break;
