@@ -677,10 +677,12 @@ def main() -> int:
             checkpoint.write_chronos2(ckpt, c4, synthetic.c2_portable_weights(c4, seed=0))
             series, n_targets = c4_series()
             # fp32 first: the encoder inside config 4's 1e-3 quantile bar
-            also["c2_forecast_f32"] = forecast_line(ckpt, series, n_targets, "f32", cpu=want_cpu)
+            also["c2_forecast_f32"] = forecast_line(ckpt, series, n_targets, "f32")
             # f16x3: fp16 GEMMs over three-term splits, inside the same 1e-3 bar
             also["c2_forecast_f16x3"] = forecast_line(ckpt, series, n_targets, "f16x3")
             also["c2_forecast_bf16"] = forecast_line(ckpt, series, n_targets, "bf16")
+            if want_cpu:  # the oracle's forward, after the device forecasts
+                also["c2_forecast_f32"]["cpu_baseline"] = forecast_cpu_baseline(ckpt, series, cpu_threads())
         finally:
             shutil.rmtree(ckpt, ignore_errors=True)
         if args.only == "forecast":
