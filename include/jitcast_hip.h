@@ -92,6 +92,12 @@ int jc_plan_end(jc_ctx *ctx, jc_plan **plan);
 /* Replays the plan on the context's current stream (asynchronous; jc_sync waits). */
 int jc_plan_launch(jc_plan *plan);
 /*
+ * Replays the plan on `hip_stream` (NULL: the stream of the context that captured it), whichever
+ * stream that context launches on now; for a host whose threads each keep their own context and
+ * share plans, as one PlanCache serves every caller of an engine (J/tornado/PlanCache.java:70-100).
+ */
+int jc_plan_launch_on(jc_plan *plan, void *hip_stream);
+/*
  * Gives the plan ownership of a device buffer from jc_alloc: jc_plan_destroy frees it and
  * jc_plan_device_bytes counts it, as each TornadoVM plan counts its own buffers (PlanCache.java:30-36).
  */

@@ -28,7 +28,6 @@ struct jc_ctx {
     hipStream_t capture_on;  // the stream being captured
     uint64_t capture_key;
     jc::Blas* blas;          // hipBLASLt for the plain GEMMs (nullptr: the library's own kernels)
-    bool own_gemm;           // set while a call must not use hipBLASLt (jc_c2_layer_static)
 };
 
 struct jc_plan {
@@ -86,7 +85,7 @@ LpKernel lp_choice(bool ts) {
 // JITCAST_HIP_GEMM=own runs the plain GEMMs on the library's own MFMA kernels (gemm_f32, gemm_lp)
 // instead of hipBLASLt. Read at every call.
 bool use_blas(const jc_ctx* ctx) {
-    if (!ctx->blas || ctx->own_gemm) return false;
+    if (!ctx->blas) return false;
     const char* e = getenv("JITCAST_HIP_GEMM");
     return !(e && !strcmp(e, "own"));
 }
@@ -171,7 +170,6 @@ int jc_init(int device, jc_ctx** out) {
     ctx->capture_on = nullptr;
     ctx->capture_key = 0;
     ctx->blas = jc::blas_create();  // nullptr leaves the GEMMs on the library's own kernels
-    ctx->own_gemm = false;
     *out = ctx;
     return JC_OK;
 }
@@ -589,17 +587,25 @@ int jc_plan_end(jc_ctx* ctx, jc_plan** out) {
     return JC_OK;
 }
 
-int jc_plan_launch(jc_plan* plan) {
-    if (!plan) return fail(JC_EINVAL, "jc_plan_launch: null plan");
-    int rc = use(plan->ctx, "jc_plan_launch");
+static int plan_launch(jc_plan* plan, hipStream_t stream, const char* W) {
+    if (!plan) return fail(JC_EINVAL, "%s: null plan", W);
+    int rc = use(plan->ctx, W);
     if (rc) return rc;
-    if (plan->ctx->capturing) return fail(JC_ESTATE, "jc_plan_launch: the context is capturing a plan");
-    hipError_t e = hipGraphLaunch(plan->exec, plan->ctx->stream);
-    if (e != hipSuccess) return hip_fail("jc_plan_launch", e);
+    if (plan->ctx->capturing) return fail(JC_ESTATE, "%s: the context is capturing a plan", W);
+    hipError_t e = hipGraphLaunch(plan->exec, stream);
+    if (e != hipSuccess) return hip_fail(W, e);
     // jc_plan_destroy waits for this event, so a replay on any stream ends before the graph and
     // its buffers are released, whatever stream the context launches on by then
-    e = hipEventRecord(plan->done, plan->ctx->stream);
-    return e == hipSuccess ? JC_OK : hip_fail("jc_plan_launch: hipEventRecord", e);
+    e = hipEventRecord(plan->done, stream);
+    return e == hipSuccess ? JC_OK : hip_fail(W, e);
+}
+
+int jc_plan_launch(jc_plan* plan) {
+    return plan_launch(plan, plan ? plan->ctx->stream : nullptr, "jc_plan_launch");
+}
+
+int jc_plan_launch_on(jc_plan* plan, void* stream) {
+    return plan_launch(plan, stream ? (hipStream_t)stream : (plan ? plan->ctx->stream : nullptr), "jc_plan_launch_on");
 }
 
 int jc_plan_adopt(jc_plan* plan, void* dptr, size_t bytes) {
@@ -803,12 +809,11 @@ int jc_c2_layer_static(jc_ctx* ctx, float* x, const jc_c2_layer_weights* w, cons
                     W, rows, n, (long long)need, (long long)JC_C2_LAYER_STATIC_BYTES);
     void* ws = scratch_ptr(ctx->device);
     if (!ws) return fail(JC_EUNSUPPORTED, "%s: no static scratch on device %d", W, ctx->device);
-    // the library's own GEMM kernels: no library routine that could allocate
-    ctx->own_gemm = true;
-    const int rc = c2_layer(ctx, W, x, w, live, table, group_start, group_end, ws, rows, n, d, heads, dh, dff, eps,
-                            dtype);
-    ctx->own_gemm = false;
-    return rc;
+    // the library's own GEMM kernels, so no library routine that could allocate runs: the layer runs
+    // on a copy of the context without hipBLASLt, which leaves the caller's context untouched
+    jc_ctx own = *ctx;
+    own.blas = nullptr;
+    return c2_layer(&own, W, x, w, live, table, group_start, group_end, ws, rows, n, d, heads, dh, dff, eps, dtype);
 }
 
 // ---- bf16 / fp16 layer ------------------------------------------------------------------------

@@ -9,18 +9,30 @@
 // declined too: the reference's FP16 twins saturate to +-65504 (Kernels.java:42-46), hipBLASLt's
 // conversion does not.
 //
-// Per context: one handle and one workspace (made by jc_init), and a cache of descriptors and the
-// heuristic's first algorithm per GEMM shape, so a call costs one descriptor update and the launch.
+// Results are reproducible: a plan replays the same task graph as the eager forward
+// (J/chronos2/tornado/Chronos2Forward.java:292-300), so the same GEMM on the same operands must give
+// the same bits whenever and on whichever stream it runs. On gfx950 hipBLASLt's kernels are Stream-K
+// kernels ("..._SK3_..."): given a workspace, one may split a tile's k range over workgroups and
+// combine the partial tiles through it. Only algorithms whose heuristic result needs no workspace are
+// taken, and hipblasLtMatmul gets none (a null pointer and 0 bytes), so every tile of C is computed by
+// one workgroup in a fixed order over k. A test checks that consequence: permuting the rows of A
+// permutes the rows of C bit for bit, which a split k range would not keep.
+//
+// Per context: one handle and a cache of descriptors and the chosen algorithm per GEMM shape, so a
+// call costs one descriptor update and the launch.
 #include "jc_blas.hpp"
 
+#include <hipblaslt/hipblaslt-ext.hpp>
 #include <hipblaslt/hipblaslt.h>
 
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <new>
+#include <string>
 #include <unordered_map>
 #include <unordered_set>
+#include <vector>
 
 #include "../../include/jitcast_hip.h"
 
@@ -45,7 +57,7 @@ struct Entry {
     hipblasLtMatmulDesc_t desc = nullptr;
     hipblasLtMatrixLayout_t lw = nullptr, la = nullptr, lc = nullptr;
     hipblasLtMatmulAlgo_t algo{};
-    bool ok = false;  // the heuristic found an algorithm
+    bool ok = false;  // the heuristic offered a reproducible algorithm
 };
 
 hipDataType hip_type(int dtype) {
@@ -60,9 +72,6 @@ constexpr int kZeroBias = 1 << 16;
 
 struct Blas {
     hipblasLtHandle_t handle = nullptr;
-    void* ws = nullptr;
-    size_t ws_bytes = 0;
-    size_t ws_limit = 0;  // the most workspace an algorithm may ask for (JITCAST_HIP_BLAS_WORKSPACE)
     float* zeros = nullptr;  // kZeroBias floats
     std::unordered_map<Key, Entry, KeyHash> cache;
     std::unordered_set<uint64_t> reported;  // declined shapes already reported (JITCAST_HIP_BLAS_DEBUG)
@@ -75,21 +84,9 @@ Blas* blas_create() {
         delete b;
         return nullptr;
     }
-    b->ws_bytes = kBlasWorkspaceBytes;
-    b->ws_limit = b->ws_bytes;
-    if (const char* e = getenv("JITCAST_HIP_BLAS_WORKSPACE")) {
-        const unsigned long long v = strtoull(e, nullptr, 10);
-        b->ws_limit = v < b->ws_bytes ? (size_t)v : b->ws_bytes;
-    }
-    if (hipMalloc(&b->ws, b->ws_bytes) != hipSuccess) {
-        (void)hipblasLtDestroy(b->handle);
-        delete b;
-        return nullptr;
-    }
     if (hipMalloc(&b->zeros, kZeroBias * sizeof(float)) != hipSuccess ||
         hipMemset(b->zeros, 0, kZeroBias * sizeof(float)) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
         (void)hipFree(b->zeros);
-        (void)hipFree(b->ws);
         (void)hipblasLtDestroy(b->handle);
         delete b;
         return nullptr;
@@ -107,9 +104,18 @@ void blas_destroy(Blas* b) {
         if (e.lc) (void)hipblasLtMatrixLayoutDestroy(e.lc);
     }
     (void)hipFree(b->zeros);
-    (void)hipFree(b->ws);
     (void)hipblasLtDestroy(b->handle);
     delete b;
+}
+
+// JITCAST_HIP_BLAS_DEBUG=1 reports on stderr the kernel chosen for each GEMM shape and each shape this
+// path declines, once per shape and context.
+static bool debug_on() {
+    static const bool on = [] {
+        const char* e = getenv("JITCAST_HIP_BLAS_DEBUG");
+        return e && *e == '1';
+    }();
+    return on;
 }
 
 static Entry* entry_for(Blas* b, const Key& key) {
@@ -125,8 +131,12 @@ static Entry* entry_for(Blas* b, const Key& key) {
                hipblasLtMatmulDescSetAttribute(e.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof tb) == 0 &&
                hipblasLtMatmulDescSetAttribute(e.desc, HIPBLASLT_MATMUL_DESC_EPILOGUE, &epi, sizeof epi) == 0;
         if (good && (key.epi & HIPBLASLT_EPILOGUE_BIAS)) {
+            // the support check below wants a bias pointer; each call sets its own before the launch
             const hipDataType bt = HIP_R_32F;
-            good = hipblasLtMatmulDescSetAttribute(e.desc, HIPBLASLT_MATMUL_DESC_BIAS_DATA_TYPE, &bt, sizeof bt) == 0;
+            const float* placeholder = b->zeros;
+            good = hipblasLtMatmulDescSetAttribute(e.desc, HIPBLASLT_MATMUL_DESC_BIAS_DATA_TYPE, &bt, sizeof bt) == 0 &&
+                   hipblasLtMatmulDescSetAttribute(e.desc, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &placeholder,
+                                                   sizeof placeholder) == 0;
         }
     }
     // W: column-major k x n (ld k); A: column-major k x m (ld lda); C: column-major n x m (ld ldc)
@@ -136,18 +146,49 @@ static Entry* entry_for(Blas* b, const Key& key) {
     if (good) {
         hipblasLtMatmulPreference_t pref = nullptr;
         if (hipblasLtMatmulPreferenceCreate(&pref) == 0) {
-            const uint64_t wsb = b->ws_limit;
-            constexpr int kAsk = 8;
-            hipblasLtMatmulHeuristicResult_t res[kAsk];
+            // the heuristic ranks its candidates as if any workspace were available; each one's need for
+            // this very problem then comes from matmulIsAlgoSupported, and the first that needs none is
+            // taken. The choice is a function of the shape alone: every context and process makes it.
+            const uint64_t rank_as_if = 1ull << 30;
+            // deep enough that a workspace-free candidate turns up: for config 4's fp32 shapes the
+            // first one ranks 9th to 50th, within 0-11% of the heuristic's first choice
+            constexpr int kAsk = 512;
+            std::vector<hipblasLtMatmulHeuristicResult_t> res;
+            try {
+                res.resize(kAsk);
+            } catch (...) {
+                res.clear();
+            }
             int got = 0;
-            if (hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsb,
-                                                      sizeof wsb) == 0 &&
-                hipblasLtMatmulAlgoGetHeuristic(b->handle, e.desc, e.lw, e.la, e.lc, e.lc, pref, kAsk, res, &got) == 0) {
-                for (int i = 0; i < got; i++) {  // the heuristic's order: the first that fits the workspace
-                    if (res[i].workspaceSize <= b->ws_limit) {
-                        e.algo = res[i].algo;
-                        e.ok = true;
-                        break;
+            const float alpha = 1.f, beta = key.acc ? 1.f : 0.f;
+            if (hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &rank_as_if,
+                                                      sizeof rank_as_if) == 0 &&
+                !res.empty() &&
+                hipblasLtMatmulAlgoGetHeuristic(b->handle, e.desc, e.lw, e.la, e.lc, e.lc, pref, kAsk, res.data(), &got) == 0) {
+                int skipped = 0;
+                for (int i = 0; i < got && !e.ok; i++) {
+                    size_t need = 1;
+                    const hipblasStatus_t sup =
+                        res[i].state != HIPBLAS_STATUS_SUCCESS
+                            ? res[i].state
+                            : hipblaslt_ext::matmulIsAlgoSupported(b->handle, e.desc, &alpha, e.lw, e.la, &beta, e.lc,
+                                                                   e.lc, res[i].algo, need);
+                    if (sup != HIPBLAS_STATUS_SUCCESS || need != 0) {
+                        skipped++;
+                        continue;
+                    }
+                    e.algo = res[i].algo;
+                    e.ok = true;
+                    if (debug_on()) {
+                        std::string name;
+                        try {
+                            name = hipblaslt_ext::getKernelNameFromAlgo(b->handle, e.algo);
+                        } catch (...) {
+                            name = "?";
+                        }
+                        fprintf(stderr, "[jc_blas] m=%d n=%d k=%d ab=%d c=%d epi=%d acc=%d: %s (candidate %d of %d; %d "
+                                "skipped: unsupported or needing a workspace)\n", key.m, key.n, key.k, key.ab, key.cd,
+                                key.epi, key.acc, name.c_str(), i + 1, got, skipped);
                     }
                 }
             }
@@ -159,15 +200,6 @@ static Entry* entry_for(Blas* b, const Key& key) {
     } catch (...) {
         return nullptr;
     }
-}
-
-// JITCAST_HIP_BLAS_DEBUG=1 reports on stderr each GEMM shape this path declines, once per shape and context.
-static bool debug_on() {
-    static const bool on = [] {
-        const char* e = getenv("JITCAST_HIP_BLAS_DEBUG");
-        return e && *e == '1';
-    }();
-    return on;
 }
 
 static BlasStatus decline(Blas* b, const char* why, int m, int n, int k, int flags, int ab, int cd) {
@@ -210,7 +242,7 @@ BlasStatus blas_gemm(Blas* b, const void* a, int lda, const void* w, const float
         return kBlasError;
     const float alpha = 1.f, beta = acc ? 1.f : 0.f;
     const hipblasStatus_t s = hipblasLtMatmul(b->handle, e->desc, &alpha, w, e->lw, a, e->la, &beta, c, e->lc, c,
-                                              e->lc, &e->algo, b->ws, b->ws_bytes, stream);
+                                              e->lc, &e->algo, nullptr, 0, stream);
     return s == HIPBLAS_STATUS_SUCCESS ? kBlasDone : kBlasError;
 }
 

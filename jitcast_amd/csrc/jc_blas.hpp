@@ -9,18 +9,16 @@ namespace jc {
 
 struct Blas;
 
-// device workspace per context for hipBLASLt's algorithms (split-K partial sums and the like)
-constexpr size_t kBlasWorkspaceBytes = 32u << 20;
-
 enum BlasStatus { kBlasDone, kBlasDecline, kBlasError };
 
-// A handle and its workspace on the current device; nullptr when hipBLASLt cannot start.
+// A handle on the current device; nullptr when hipBLASLt cannot start.
 Blas* blas_create();
 void blas_destroy(Blas* b);
 
 // C[m, n] (+)= act(A[m, :k] . W[n, :k]^T + bias[n]) (row-major; flags as Kernels.gemm's) on `stream`.
 // kBlasDecline: a combination this path does not take (an activation with ACCUMULATE, fp16 output,
-// no algorithm for the shape); the caller runs its own kernel.
+// no reproducible algorithm for the shape); the caller runs its own kernel. Same operands, same bits:
+// only algorithms that run without a workspace are used, and none is given.
 BlasStatus blas_gemm(Blas* b, const void* a, int lda, const void* w, const float* bias, void* c, int ldc, int m, int n,
                      int k, int flags, int ab_dtype, int c_dtype, hipStream_t stream);
 

@@ -4,7 +4,7 @@ The reference compiles one TornadoVM execution plan per input shape and keeps th
 (J/tornado/PlanCache.java:40-161): at most `max_plans`, within `max_bytes` of device memory, least
 recently used evicted first, a failed first run retried once after clearing the cache. Here a plan
 is a hipGraph captured from the library's entry points (jc_plan_begin / jc_plan_end), replayed with
-jc_plan_launch; the device buffers a plan adopts are its footprint.
+jc_plan_launch_on; the device buffers a plan adopts are its footprint.
 """
 from __future__ import annotations
 
@@ -21,16 +21,19 @@ from .runtime import context
 class Plan:
     """A captured, instantiated hipGraph (jc_plan) of one device."""
 
-    def __init__(self, handle: ctypes.c_void_p, device: int = 0):
+    def __init__(self, handle: ctypes.c_void_p, device: int = 0, ctx=None):
         self.handle = handle
         self.device = device
+        self._ctx = ctx  # the capturing context: the plan refers to it, so it must outlive the plan
 
     def launch(self) -> None:
-        """Replays the graph on torch's current stream: jc_plan_launch launches on the stream its
-        context is bound to, so the context is bound to the current stream first (the last binding
-        may have been to another stream, such as the one a capture ran on)."""
-        context(self.device)
-        _lib.call("jc_plan_launch", self.handle)
+        """Replays the graph on torch's current stream (jc_plan_launch_on), from any thread: the
+        plan keeps the context of the thread that captured it, and that context's binding is
+        neither read nor changed."""
+        import torch
+
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        _lib.call("jc_plan_launch_on", self.handle, ctypes.c_void_p(stream))
 
     def adopt(self, dptr: int, nbytes: int) -> None:
         """Hands a jc_alloc buffer to the plan: freed by close(), counted by device_bytes()."""
@@ -67,7 +70,7 @@ def capture(shape_key: int, device: int = 0):
     finally:
         h = ctypes.c_void_p()
         _lib.call("jc_plan_end", ctx.handle, ctypes.byref(h))
-        box.append(Plan(h, device))
+        box.append(Plan(h, device, ctx))
 
 
 K = TypeVar("K", bound=Hashable)

@@ -1,4 +1,4 @@
-"""The device context: one jc_ctx per device, launching on torch's current stream.
+"""The device context: one jc_ctx per device and thread, launching on torch's current stream.
 
 PyTorch is plumbing here (device memory and streams); every computation on the attention path
 runs in libjitcast_hip.
@@ -6,6 +6,7 @@ runs in libjitcast_hip.
 from __future__ import annotations
 
 import ctypes
+import threading
 
 from . import _lib
 
@@ -53,14 +54,21 @@ class HipContext:
             pass
 
 
-_default: dict[int, HipContext] = {}
+_local = threading.local()
 
 
 def context(device: int = 0) -> HipContext:
-    """The process-wide context of a device, bound to torch's current stream on every call."""
-    ctx = _default.get(device)
+    """The calling thread's context on a device, bound to torch's current stream on every call.
+
+    Each thread keeps its own jc_ctx (its own stream binding and hipBLASLt handle), so engines used
+    from different threads never launch on each other's streams: a context's binding only changes
+    between the calls of the one thread that owns it."""
+    ctxs = getattr(_local, "ctxs", None)
+    if ctxs is None:
+        ctxs = _local.ctxs = {}
+    ctx = ctxs.get(device)
     if ctx is None:
-        ctx = _default[device] = HipContext(device)
+        ctx = ctxs[device] = HipContext(device)
     ctx.bind_torch_stream()
     return ctx
 

@@ -148,14 +148,6 @@ def _c4_weights():
     return _cache["c4w"]
 
 
-def _oracle_forecast(oracle, c, w, lay):
-    tok, loc, scale = oracle.c2_prep(lay.window, lay.future, lay.nc, lay.h, c.patch_size, c.time_encoding_scale,
-                                     c.use_arcsinh)
-    raw = oracle.c2_forward_raw(tok, w, lay.live, lay.group, lay.rows, lay.nc, lay.nreg, lay.h, c.num_heads, c.d_kv,
-                                c.layer_norm_eps, c.rope_theta)
-    return oracle.c2_finish(raw, loc, scale, lay.rows, lay.h, c.num_quantiles, c.patch_size, c.use_arcsinh)
-
-
 @pytest.mark.parametrize("dt", ["f32", "f16x3", "bf16", "fp16"])
 def test_config4_forecast_matches_oracle(gpu, oracle, dt):
     groups, h = 2, 4
@@ -163,8 +155,8 @@ def test_config4_forecast_matches_oracle(gpu, oracle, dt):
     ctx, group, fut, _ = synthetic.c2_forecast_config4(groups=groups, seed=7)
     w = _c4_weights()
     if "c4exp" not in _cache:
-        lay = cm.layout(C4, ctx, group, fut, h=h)
-        _cache["c4exp"] = _oracle_forecast(oracle, C4, w, lay)
+        # the oracle's own ModelLayout.of, ModelPrep and forward (oracle.c2_model_forward), not the product's
+        _cache["c4exp"] = oracle.c2_model_forward(C4, w, ctx, group, fut, h)
     exp = _cache["c4exp"]
     model = cm.HipChronos2Model(C4, w, dtype=dt)
     got = model.forecast(ctx, group, fut, h=h)
@@ -175,11 +167,38 @@ def test_config4_forecast_matches_oracle(gpu, oracle, dt):
     assert err <= bar
 
 
+@pytest.mark.parametrize("dt", ["bf16", "f32"])
+def test_config4_call_reproducible(gpu, dt):
+    """One of config 4's forward calls (52 groups x 5 rows x 2048 steps: 260 rows of 133 tokens through
+    the 120M-class encoder) forecast eagerly and from its plan, three times each, with another engine's
+    GEMMs (other hipBLASLt algorithms) run in between: every forecast is bit-identical to the first. A
+    plan replays the eager task graph (J/chronos2/tornado/Chronos2Forward.java:292-300)."""
+    print(f"case config 4 call reproducible {dt}: 52 groups x 5 rows, h=4", flush=True)
+    ctx, group, fut, _ = synthetic.c2_forecast_config4(groups=52, seed=11)
+    w = _c4_weights()
+    eager = cm.HipChronos2Model(C4, w, dtype=dt)
+    planned = cm.HipChronos2Model(C4, w, dtype=dt, max_plans=1)
+    other = cm.HipChronos2Model(C4, w, dtype="f16x3" if dt == "bf16" else "bf16")
+    try:
+        first = eager.forecast(ctx, group, fut, h=4)
+        assert np.isfinite(first).all()
+        for k in range(3):
+            other.forecast(ctx[:25], group[:25], fut[:25], h=4)
+            p = planned.forecast(ctx, group, fut, h=4)
+            e = eager.forecast(ctx, group, fut, h=4)
+            torch.cuda.synchronize()
+            print(f"  round {k}: plan differs in {int((p != first).sum())} values, eager in {int((e != first).sum())}",
+                  flush=True)
+            np.testing.assert_array_equal(p, first)
+            np.testing.assert_array_equal(e, first)
+    finally:
+        planned.close()
+
+
 def test_config4_full_request_properties(gpu):
     """Config 4's full request (1,024 groups, 5,120 rows) through the fp32 encoder: finite quantiles,
-    and permuting the groups permutes the forecasts, to fp32 rounding: every kernel computes a row
-    independently of its slot, but hipBLASLt's algorithm for these GEMM shapes may give output tiles
-    different splits of k, so a row's sums can round differently where it sits."""
+    and permuting the groups permutes the forecasts bit for bit: every kernel computes a row
+    independently of its slot, the GEMMs included (no tile's k range is split over workgroups)."""
     print("case config 4 full request fp32: 1024 groups x 5 rows x 2048 steps", flush=True)
     ctx, group, fut, _ = synthetic.c2_forecast_config4()
     model = cm.HipChronos2Model(C4, _c4_weights(), dtype="f32")
@@ -190,4 +209,4 @@ def test_config4_full_request_properties(gpu):
     b = model.forecast(ctx[rows], group[rows], fut[rows], h=4)
     d = float(np.max(np.abs(a[rows].astype(np.float64) - b)) / np.max(np.abs(b)))
     print(f"  permuted groups: max rel diff {d:.2e}", flush=True)
-    assert d <= 1e-5
+    np.testing.assert_array_equal(a[rows], b)

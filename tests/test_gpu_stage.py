@@ -54,6 +54,42 @@ def test_linear_matches_oracle(gpu, oracle, gemm_path, m, n, k, flags, bias):
     assert oracle.rel_max_error(c.cpu().numpy(), exp) <= 1e-5
 
 
+@pytest.mark.parametrize("dt,n,k,flags,out", [
+    ("f32", 2304, 768, 0, "f32"), ("f32", 768, 3072, chronos2.GEMM_ACCUMULATE, "f32"),
+    ("bf16", 2304, 768, 0, "lp"), ("bf16", 3072, 768, chronos2.GEMM_RELU, "lp"),
+    ("bf16", 768, 768, chronos2.GEMM_ACCUMULATE, "f32")])
+def test_gemm_rows_are_independent(gpu, gemm_path, dt, n, k, flags, out):
+    """Config 4's GEMM shapes (m = 260 rows x 133 tokens = 34,580): permuting the rows of A (and of C
+    for ACCUMULATE) permutes the rows of C bit for bit, and a repeated call gives the same bits. Each
+    tile of C is then one workgroup's fixed-order sum over k, wherever a row sits: the property that
+    keeps forecasts reproducible. A GEMM that splits a tile's k range over workgroups and adds the
+    partial tiles (hipBLASLt's Stream-K kernels given a workspace) changes a row's rounding with its
+    position."""
+    m = 260 * 133
+    print(f"case {dt} m={m} n={n} k={k} flags={flags} out={out}", flush=True)
+    r = np.random.default_rng(n + k + flags)
+    tdt = torch.float32 if dt == "f32" else LP[dt]
+    a = _t(r.standard_normal((m, k)).astype(np.float32)).to(tdt)
+    w = _t((r.standard_normal((n, k)) / np.sqrt(k)).astype(np.float32)).to(tdt)
+    c0 = _t(r.standard_normal((m, n)).astype(np.float32))
+    perm = torch.from_numpy(np.random.default_rng(7).permutation(m)).to(DEV)
+    run = chronos2.linear if dt == "f32" else chronos2.linear_lp
+
+    def gemm(a_, c_init):
+        c = c_init.clone() if out == "f32" else torch.empty(m, n, dtype=tdt, device=DEV)
+        run(a_, w, c, flags=flags)
+        return c
+
+    first = gemm(a, c0)
+    again = gemm(a, c0)
+    permuted = gemm(a[perm].contiguous(), c0[perm].contiguous())
+    torch.cuda.synchronize()
+    assert torch.equal(first, again)
+    diff = int((first[perm] != permuted).sum())
+    print(f"  permuted rows: {diff} values differ", flush=True)
+    assert diff == 0
+
+
 def test_linear_strided_operands(gpu, oracle, gemm_path):
     """lda > k (a column slice of a wider activation) and ldc > n (writing into a wider buffer)."""
     m, n, k, lda, ldc = 70, 48, 32, 40, 64
