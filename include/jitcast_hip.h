@@ -63,6 +63,19 @@ int jc_destroy(jc_ctx *ctx);
 int jc_set_stream(jc_ctx *ctx, void *hip_stream);
 /* The stream launches go to. */
 void *jc_stream(jc_ctx *ctx);
+/*
+ * Per-kernel timing, the counterpart of -Dchronos2.tornado.profile and -Dtimestral.tornado.profile
+ * (J/chronos2/tornado/Chronos2Forward.java:301-303, J/timestral/tornado/TimestralForward.java:391-393,
+ * TornadoVM's console profiler). on = 1 starts (or restarts) recording a HIP event pair around every
+ * launch the context makes outside a capture; on = 0 stops and discards.
+ */
+int jc_profile(jc_ctx *ctx, int on);
+/*
+ * Waits for the context's stream, writes one line per kernel (calls, total, mean, min and max ms,
+ * the largest total first) into buf as text, and clears what was recorded. JC_ESTATE when profiling
+ * is off.
+ */
+int jc_profile_report(jc_ctx *ctx, char *buf, size_t len);
 int jc_alloc(jc_ctx *ctx, size_t bytes, void **dptr);
 int jc_free(jc_ctx *ctx, void *dptr);
 int jc_memcpy_h2d(jc_ctx *ctx, void *dst, const void *src, size_t bytes);

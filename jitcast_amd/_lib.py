@@ -57,6 +57,8 @@ SIGNATURES = {
     "jc_plan_end": (_i, [_vp, _c.POINTER(_vp)]),
     "jc_plan_launch": (_i, [_vp]),
     "jc_plan_launch_on": (_i, [_vp, _vp]),
+    "jc_profile": (_i, [_vp, _i]),
+    "jc_profile_report": (_i, [_vp, _c.c_char_p, _sz]),
     "jc_plan_adopt": (_i, [_vp, _vp, _sz]),
     "jc_plan_device_bytes": (_c.c_int64, [_vp]),
     "jc_plan_key": (_c.c_uint64, [_vp]),

@@ -24,7 +24,8 @@ from dataclasses import dataclass, field
 
 import numpy as np
 
-from . import _lib, chronos2
+from . import _lib, chronos2, runtime
+from . import options as opts
 from . import plans as plans_mod
 
 QUANTILES_21 = (0.01, 0.05, 0.1, 0.15, 0.2, 0.25, 0.3, 0.35, 0.4, 0.45, 0.5, 0.55, 0.6, 0.65, 0.7, 0.75, 0.8, 0.85,
@@ -256,6 +257,8 @@ class HipChronos2Model:
                     d[k] = lp
             self.layers.append(d)
         self._bufs = {}
+        # -Dchronos2.hip.profile: per-kernel times of each eager forward, the time of each plan replay
+        self.profile = opts.boolean("chronos2.hip.profile", False)
         self.plans = None
         if max_plans > 0:
             self.plans = plans_mod.PlanCache(max_plans, plan_bytes if plan_bytes else 1 << 62)
@@ -295,6 +298,11 @@ class HipChronos2Model:
         output patch embedding [rows*h, Q*P] on the GPU; rows grouped contiguously. bufs: a plan's
         buffers (default: the eager forward's). sink(name, x), when given, sees the encoder's x after
         each layer ("layer0", ...), as the reference's StageSink (CpuChronos2.java:160)."""
+        label = f"chronos2.hip.profile forward rows={rows} n={nc + (1 if self.c.use_reg_token else 0) + h}"
+        with runtime.kernel_profile(self.dev.index or 0, label, self.profile):
+            return self._forward_raw(tokens, live, group_start, group_end, rows, nc, h, bufs, sink)
+
+    def _forward_raw(self, tokens, live, group_start, group_end, rows: int, nc: int, h: int, bufs, sink):
         c = self.c
         nreg = 1 if c.use_reg_token else 0
         n, ne, d, ff = nc + nreg + h, nc + h, c.d_model, c.d_ff
@@ -367,7 +375,7 @@ class HipChronos2Model:
             b["live"].copy_(live)
             b["gs"].copy_(up(gs))
             b["ge"].copy_(up(ge))
-            plan.graph.launch()
+            runtime.timed_replay(f"chronos2.hip.profile rows={rows} nc={nc} h={h}", self.profile, plan.graph.launch)
             out = torch.empty(rows, c.num_quantiles, h * c.patch_size, dtype=torch.float32, device=dev)
             chronos2.finish(b["raw"], loc, scale, ord_t, rows, h, c.num_quantiles, c.patch_size, c.use_arcsinh, out)
             return out.cpu().numpy()

@@ -11,7 +11,10 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <algorithm>
+#include <map>
 #include <mutex>
+#include <string>
 #include <new>
 #include <vector>
 
@@ -28,6 +31,13 @@ struct jc_ctx {
     hipStream_t capture_on;  // the stream being captured
     uint64_t capture_key;
     jc::Blas* blas;          // hipBLASLt for the plain GEMMs (nullptr: the library's own kernels)
+    std::vector<struct jc_prof_record>* prof;  // per-kernel timing (jc_profile), nullptr when off
+};
+
+// One timed launch: HIP events on the context's stream before and after it.
+struct jc_prof_record {
+    const char* name;
+    hipEvent_t a, b;
 };
 
 struct jc_plan {
@@ -66,6 +76,55 @@ int use(jc_ctx* ctx, const char* where) {
 }
 
 size_t dtype_size(int dtype) { return dtype == JC_F32 ? 4 : 2; }
+
+// Times the launches made in its scope when the context profiles (jc_profile) and its stream is not
+// being captured: an event before, one after, kept until jc_profile_report reads them.
+class ProfScope {
+  public:
+    ProfScope(jc_ctx* ctx, const char* name) {
+        if (!ctx || !ctx->prof) return;
+        hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(ctx->stream, &st) != hipSuccess || st != hipStreamCaptureStatusNone) return;
+        if (hipEventCreate(&rec_.a) != hipSuccess) return;
+        if (hipEventCreate(&rec_.b) != hipSuccess || hipEventRecord(rec_.a, ctx->stream) != hipSuccess) {
+            (void)hipEventDestroy(rec_.a);
+            if (rec_.b) (void)hipEventDestroy(rec_.b);
+            return;
+        }
+        rec_.name = name;
+        ctx_ = ctx;
+    }
+    ~ProfScope() {
+        if (!ctx_) return;
+        bool kept = hipEventRecord(rec_.b, ctx_->stream) == hipSuccess;
+        if (kept) {
+            try {
+                ctx_->prof->push_back(rec_);
+            } catch (...) {
+                kept = false;
+            }
+        }
+        if (!kept) {
+            (void)hipEventDestroy(rec_.a);
+            (void)hipEventDestroy(rec_.b);
+        }
+    }
+    ProfScope(const ProfScope&) = delete;
+    ProfScope& operator=(const ProfScope&) = delete;
+
+  private:
+    jc_ctx* ctx_ = nullptr;
+    jc_prof_record rec_{nullptr, nullptr, nullptr};
+};
+
+void prof_clear(jc_ctx* ctx) {
+    if (!ctx->prof) return;
+    for (auto& r : *ctx->prof) {
+        (void)hipEventDestroy(r.a);
+        (void)hipEventDestroy(r.b);
+    }
+    ctx->prof->clear();
+}
 
 // JITCAST_HIP_LP_KERNEL picks the bf16/fp16 time-attention kernel: "stream" (time_attention_lp,
 // which takes every shape), "wide" (time_attention_lpw) or "persist" (time_attention_lpp), the
@@ -170,6 +229,7 @@ int jc_init(int device, jc_ctx** out) {
     ctx->capture_on = nullptr;
     ctx->capture_key = 0;
     ctx->blas = jc::blas_create();  // nullptr leaves the GEMMs on the library's own kernels
+    ctx->prof = nullptr;
     *out = ctx;
     return JC_OK;
 }
@@ -183,6 +243,10 @@ int jc_destroy(jc_ctx* ctx) {
         ctx->capturing = false;
     }
     (void)hipStreamSynchronize(ctx->stream);
+    if (ctx->prof) {
+        prof_clear(ctx);
+        delete ctx->prof;
+    }
     jc::blas_destroy(ctx->blas);
     (void)hipStreamDestroy(ctx->own);
     delete ctx;
@@ -198,6 +262,72 @@ int jc_set_stream(jc_ctx* ctx, void* stream) {
 }
 
 void* jc_stream(jc_ctx* ctx) { return ctx ? (void*)ctx->stream : nullptr; }
+
+int jc_profile(jc_ctx* ctx, int on) {
+    int rc = use(ctx, "jc_profile");
+    if (rc) return rc;
+    if (ctx->prof) {
+        (void)hipStreamSynchronize(ctx->stream);
+        prof_clear(ctx);
+    }
+    if (!on) {
+        delete ctx->prof;
+        ctx->prof = nullptr;
+        return JC_OK;
+    }
+    if (!ctx->prof) {
+        ctx->prof = new (std::nothrow) std::vector<jc_prof_record>();
+        if (!ctx->prof) return fail(JC_ENOMEM, "jc_profile: out of host memory");
+    }
+    return JC_OK;
+}
+
+int jc_profile_report(jc_ctx* ctx, char* buf, size_t len) {
+    const char* W = "jc_profile_report";
+    int rc = use(ctx, W);
+    if (rc) return rc;
+    if (!buf || len == 0) return fail(JC_EINVAL, "%s: null or empty buffer", W);
+    buf[0] = 0;
+    if (!ctx->prof) return fail(JC_ESTATE, "%s: profiling is off (jc_profile(ctx, 1) first)", W);
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) return hip_fail(W, e);
+    struct Sum {
+        int calls = 0;
+        double total = 0, lo = 1e30, hi = 0;
+    };
+    std::map<std::string, Sum> by;
+    double all = 0;
+    int n = 0;
+    try {
+        for (const auto& r : *ctx->prof) {
+            float ms = 0.f;
+            if (hipEventElapsedTime(&ms, r.a, r.b) != hipSuccess) continue;
+            Sum& s = by[r.name];
+            s.calls++;
+            s.total += ms;
+            s.lo = std::min(s.lo, (double)ms);
+            s.hi = std::max(s.hi, (double)ms);
+            all += ms;
+            n++;
+        }
+        std::vector<std::pair<std::string, Sum>> rows(by.begin(), by.end());
+        std::sort(rows.begin(), rows.end(), [](const auto& x, const auto& y) { return x.second.total > y.second.total; });
+        size_t at = (size_t)snprintf(buf, len, "%-34s %7s %11s %10s %10s %10s\n", "kernel", "calls", "total ms", "mean ms",
+                                     "min ms", "max ms");
+        for (const auto& row : rows) {
+            if (at >= len) break;
+            const Sum& s = row.second;
+            at += (size_t)snprintf(buf + at, len - at, "%-34s %7d %11.4f %10.4f %10.4f %10.4f\n", row.first.c_str(),
+                                   s.calls, s.total, s.total / s.calls, s.lo, s.hi);
+        }
+        if (at < len) snprintf(buf + at, len - at, "%-34s %7d %11.4f\n", "all timed launches", n, all);
+    } catch (...) {
+        prof_clear(ctx);
+        return fail(JC_ENOMEM, "%s: out of host memory", W);
+    }
+    prof_clear(ctx);
+    return JC_OK;
+}
 
 int jc_alloc(jc_ctx* ctx, size_t bytes, void** dptr) {
     int rc = use(ctx, "jc_alloc");
@@ -336,12 +466,16 @@ static int launch_time(jc_ctx* ctx, const char* W, const jc::TimeArgs& a, int dh
     hipError_t e;
     const bool fp16 = dtype == JC_F16;
     if (dtype == JC_F32) {
+        ProfScope ps(ctx, ts ? "ts time_attention_f32" : "c2 time_attention_f32");
         e = jc::time_attention_f32_launch(a, dh, ts, ctx->stream);
     } else if (lp_choice(ts) == kLpPersist && jc::time_attention_lpp_fits(a, dh, ts)) {
+        ProfScope ps(ctx, ts ? "ts time_attention_lpp" : "c2 time_attention_lpp");
         e = jc::time_attention_lpp_launch(a, fp16, ctx->cus, ctx->stream);
     } else if (lp_choice(ts) != kLpStream && jc::time_attention_lpw_fits(a, dh)) {
+        ProfScope ps(ctx, ts ? "ts time_attention_lpw" : "c2 time_attention_lpw");
         e = jc::time_attention_lpw_launch(a, dh, ts, fp16, ctx->stream);
     } else {
+        ProfScope ps(ctx, ts ? "ts time_attention_lp" : "c2 time_attention_lp");
         e = jc::time_attention_lp_launch(a, dh, ts, fp16, ctx->stream);
     }
     return e == hipSuccess ? JC_OK : hip_fail(W, e);
@@ -369,6 +503,7 @@ static int c2_time(jc_ctx* ctx, const char* W, const void* qkv, void* out, const
     a.qscale = 1.4426950408889634f;  // unscaled scores, exp via exp2
     if (x3) {
         if (dtype != JC_F32) return fail(JC_EINVAL, "%s: the split output needs fp32", W);
+        ProfScope ps(ctx, "c2 time_attention_f32 (split out)");
         hipError_t e = jc::time_attention_f32_x3_launch(a, dh, ctx->stream);
         return e == hipSuccess ? JC_OK : hip_fail(W, e);
     }
@@ -446,6 +581,7 @@ int jc_ts_gate(jc_ctx* ctx, void* att, const void* g, int64_t count, int dtype) 
     const size_t align = dtype == JC_F32 ? 16 : 8;
     if (((uintptr_t)att % align) || ((uintptr_t)g % align))
         return fail(JC_EINVAL, "%s: att and g must be %zu-byte aligned", W, align);
+    ProfScope ps(ctx, "ts gate");
     hipError_t e = jc::gate_launch(att, g, (uint64_t)count, dtype, ctx->stream);
     return e == hipSuccess ? JC_OK : hip_fail(W, e);
 }
@@ -486,6 +622,7 @@ static int c2_group(jc_ctx* ctx, const char* W, const void* qkv, void* out, cons
     a.inner = inner;
     a.enc = n;
     a.qscale = 1.4426950408889634f;  // unscaled scores, exp via exp2
+    ProfScope ps(ctx, x3 ? "c2 group_attention_f32 (split out)" : "c2 group_attention_f32");
     hipError_t e = x3 ? jc::group_attention_f32_x3_launch(a, dh, ctx->stream)
                       : jc::group_attention_f32_launch(a, dh, false, ctx->stream);
     return e == hipSuccess ? JC_OK : hip_fail(W, e);
@@ -525,6 +662,7 @@ int jc_ts_variate_attention(jc_ctx* ctx, const void* qkv, void* out, const int32
     a.enc = enc;
     a.covariates = covariates;
     a.qscale = (float)(1.4426950408889634 / std::sqrt((double)dh));
+    ProfScope ps(ctx, "ts variate_attention_f32");
     hipError_t e = jc::group_attention_f32_launch(a, dh, true, ctx->stream);
     return e == hipSuccess ? JC_OK : hip_fail(W, e);
 }
@@ -670,12 +808,14 @@ static int launch_linear(jc_ctx* ctx, const char* W, const float* a, int lda, co
     int rc = check_linear(W, a, lda, w, bias, c, ldc, m, n, k, flags);
     if (rc || (size_t)m * n == 0) return rc;
     if (use_blas(ctx)) {
+        ProfScope ps(ctx, "gemm fp32 (hipBLASLt)");
         const jc::BlasStatus bs = jc::blas_gemm(ctx->blas, a, lda, w, bias, c, ldc, m, n, k, flags, JC_F32, JC_F32,
                                                 ctx->stream);
         if (bs == jc::kBlasDone) return JC_OK;
         if (bs == jc::kBlasError) return fail(JC_EHIP, "%s: hipblasLtMatmul failed", W);
     }
     jc::GemmArgs g{a, w, bias, c, m, n, k, lda, ldc, flags};
+    ProfScope ps(ctx, "gemm_f32");
     hipError_t e = jc::gemm_f32_launch(g, ctx->stream);
     return e == hipSuccess ? JC_OK : hip_fail(W, e);
 }
@@ -694,6 +834,7 @@ static int launch_rms(jc_ctx* ctx, const char* W, const float* x, const float* w
     if (!x || !y) return fail(JC_EINVAL, "%s: null x or y", W);
     if (d % 4) return fail(JC_EINVAL, "%s: d must be a multiple of 4 (got %d)", W, d);
     if (!aligned16(x) || !aligned16(y) || (w && !aligned16(w))) return fail(JC_EINVAL, "%s: 16-byte alignment", W);
+    ProfScope ps(ctx, "rms_norm_f32");
     hipError_t e = jc::rms_norm_f32_launch(x, y, w, rows, d, eps, ctx->stream);
     return e == hipSuccess ? JC_OK : hip_fail(W, e);
 }
@@ -845,12 +986,14 @@ static int launch_linear_lp(jc_ctx* ctx, const char* W, const void* a, int lda, 
     if (c_dtype != JC_F32 && (flags & JC_GEMM_ACCUMULATE))
         return fail(JC_EINVAL, "%s: JC_GEMM_ACCUMULATE needs an fp32 C", W);
     if (use_blas(ctx)) {
+        ProfScope ps(ctx, dtype == JC_F16 ? "gemm fp16 (hipBLASLt)" : "gemm bf16 (hipBLASLt)");
         const jc::BlasStatus bs = jc::blas_gemm(ctx->blas, a, lda, w, bias, c, ldc, m, n, k, flags, dtype, c_dtype,
                                                 ctx->stream);
         if (bs == jc::kBlasDone) return JC_OK;
         if (bs == jc::kBlasError) return fail(JC_EHIP, "%s: hipblasLtMatmul failed", W);
     }
     jc::GemmLpArgs g{a, w, bias, c, m, n, k, lda, ldc, flags};
+    ProfScope ps(ctx, dtype == JC_F16 ? "gemm_lp fp16" : "gemm_lp bf16");
     hipError_t e = jc::gemm_lp_launch(g, dtype == JC_F16, c_dtype != JC_F32, ctx->cus, ctx->stream);
     return e == hipSuccess ? JC_OK : hip_fail(W, e);
 }
@@ -872,6 +1015,7 @@ static int launch_rms_lp(jc_ctx* ctx, const char* W, const float* x, const float
     if (!x || !y) return fail(JC_EINVAL, "%s: null x or y", W);
     if (d % 4) return fail(JC_EINVAL, "%s: d must be a multiple of 4 (got %d)", W, d);
     if (!aligned16(x) || !aligned16(y) || (w && !aligned16(w))) return fail(JC_EINVAL, "%s: 16-byte alignment", W);
+    ProfScope ps(ctx, dtype == JC_F16X3 ? "rms_norm (split out)" : "rms_norm_lp");
     hipError_t e = dtype == JC_F16X3 ? jc::rms_norm_x3_launch(x, y, w, rows, d, eps, ctx->stream)
                                      : jc::rms_norm_lp_launch(x, y, w, rows, d, eps, dtype == JC_F16, ctx->stream);
     return e == hipSuccess ? JC_OK : hip_fail(W, e);
@@ -890,6 +1034,7 @@ static int launch_to_lp(jc_ctx* ctx, const char* W, const float* src, void* dst,
     if (count < 0) return fail(JC_EINVAL, "%s: negative count", W);
     if (count == 0) return JC_OK;
     if (!src || !dst) return fail(JC_EINVAL, "%s: null src or dst", W);
+    ProfScope ps(ctx, "to_lp");
     hipError_t e = jc::to_lp_launch(src, dst, (uint64_t)count, dtype == JC_F16, ctx->stream);
     return e == hipSuccess ? JC_OK : hip_fail(W, e);
 }
@@ -951,6 +1096,7 @@ static int launch_split_x3(jc_ctx* ctx, const char* W, const float* src, int ld,
     if (k % 4 || ld < k || ld % 4) return fail(JC_EINVAL, "%s: k and ld must be multiples of 4, ld >= k (k=%d ld=%d)", W, k, ld);
     if (!aligned16(src) || ((uintptr_t)dst & 7u)) return fail(JC_EINVAL, "%s: src 16-byte and dst 8-byte alignment", W);
     if (weights != 0 && weights != 1) return fail(JC_EINVAL, "%s: weights must be 0 or 1 (got %d)", W, weights);
+    ProfScope ps(ctx, "split_f16x3");
     hipError_t e = jc::split_x3_launch(src, ld, dst, rows, k, weights == 1, ctx->stream);
     return e == hipSuccess ? JC_OK : hip_fail(W, e);
 }
@@ -979,6 +1125,7 @@ static int layer_x3(jc_ctx* ctx, const char* W, float* x, const jc_c2_layer_weig
     const int F = JC_F16;
     int rc;
     auto rms3 = [&](const float* nw) -> int {
+        ProfScope ps(ctx, "rms_norm (split out)");
         hipError_t e = jc::rms_norm_x3_launch(x, a3, nw, T, d, eps, ctx->stream);
         return e == hipSuccess ? JC_OK : hip_fail(W, e);
     };
@@ -1034,6 +1181,7 @@ int jc_c2_assemble(jc_ctx* ctx, const float* emb, const float* reg, float* x, in
     if (!x || (n > nreg && !emb) || (nreg && !reg)) return fail(JC_EINVAL, "%s: null buffer", W);
     if (!aligned16(x) || (emb && !aligned16(emb)) || (reg && !aligned16(reg)))
         return fail(JC_EINVAL, "%s: 16-byte alignment", W);
+    ProfScope ps(ctx, "c2 assemble");
     hipError_t e = jc::assemble_tokens_launch(emb, reg, x, rows, nc, nreg, n, d, ctx->stream);
     return e == hipSuccess ? JC_OK : hip_fail(W, e);
 }
@@ -1056,6 +1204,7 @@ int jc_c2_prep(jc_ctx* ctx, const float* context, int64_t ld_context, int steps,
     if ((!context && steps > 0) || !tokens || !loc || !scale || !live) return fail(JC_EINVAL, "%s: null buffer", W);
     const int kept = steps < context_length ? steps : context_length;
     const int nc = (kept + patch - 1) / patch;
+    ProfScope ps(ctx, "c2 prep");
     hipError_t e = jc::c2_prep_launch(context, ld_context, steps, future, ld_future, future ? future_steps : 0, order,
                                       rows, kept, nc, h, patch, nreg, time_scale, arcsinh, tokens, loc, scale, live,
                                       ctx->stream);
@@ -1071,6 +1220,7 @@ int jc_c2_finish(jc_ctx* ctx, const float* raw, const float* loc, const float* s
         return fail(JC_EINVAL, "%s: sizes (rows=%d h=%d q=%d patch=%d)", W, rows, h, q, patch);
     if (rows == 0) return JC_OK;
     if (!raw || !loc || !scale || !out) return fail(JC_EINVAL, "%s: null buffer", W);
+    ProfScope ps(ctx, "c2 finish");
     hipError_t e = jc::c2_finish_launch(raw, loc, scale, order, rows, h, q, patch, arcsinh, out, ctx->stream);
     return e == hipSuccess ? JC_OK : hip_fail(W, e);
 }
@@ -1085,6 +1235,7 @@ int jc_c2_gather_future(jc_ctx* ctx, const float* y, float* dec, int rows, int f
     if (d % 4) return fail(JC_EINVAL, "%s: d must be a multiple of 4 (got %d)", W, d);
     if (!y || !dec) return fail(JC_EINVAL, "%s: null buffer", W);
     if (!aligned16(y) || !aligned16(dec)) return fail(JC_EINVAL, "%s: 16-byte alignment", W);
+    ProfScope ps(ctx, "c2 gather_future");
     hipError_t e = jc::gather_future_launch(y, dec, rows, fs, n, h, d, ctx->stream);
     return e == hipSuccess ? JC_OK : hip_fail(W, e);
 }
@@ -1129,6 +1280,7 @@ int jc_ts_assemble(jc_ctx* ctx, const float* emb, const float* query, float* x, 
     if (!x || (enc && !emb) || (n > enc && !query)) return fail(JC_EINVAL, "%s: null buffer", W);
     if (!aligned16(x) || (emb && !aligned16(emb)) || (query && !aligned16(query)))
         return fail(JC_EINVAL, "%s: 16-byte alignment", W);
+    ProfScope ps(ctx, "ts assemble");
     hipError_t e = jc::ts_assemble_launch(emb, query, x, rows, enc, n, d, ctx->stream);
     return e == hipSuccess ? JC_OK : hip_fail(W, e);
 }
@@ -1143,6 +1295,7 @@ int jc_ts_gather_decoder(jc_ctx* ctx, const float* y, float* dec, int rows, int 
     if (d % 4) return fail(JC_EINVAL, "%s: d must be a multiple of 4 (got %d)", W, d);
     if (!y || !dec) return fail(JC_EINVAL, "%s: null buffer", W);
     if (!aligned16(y) || !aligned16(dec)) return fail(JC_EINVAL, "%s: 16-byte alignment", W);
+    ProfScope ps(ctx, "ts gather_decoder");
     hipError_t e = jc::gather_future_launch(y, dec, rows, enc, n, h, d, ctx->stream);
     return e == hipSuccess ? JC_OK : hip_fail(W, e);
 }
@@ -1158,6 +1311,7 @@ int jc_swiglu(jc_ctx* ctx, const void* up, void* act, int64_t tokens, int f, int
     if (!up || !act) return fail(JC_EINVAL, "%s: null up or act", W);
     if (dtype == JC_F16X3 && (f % 4 || !aligned16(up) || !aligned16(act)))
         return fail(JC_EINVAL, "%s: JC_F16X3 needs f a multiple of 4 (got %d) and 16-byte alignment", W, f);
+    ProfScope ps(ctx, "swiglu");
     hipError_t e = jc::swiglu_launch(up, act, (uint64_t)tokens, f, dtype, ctx->stream);
     return e == hipSuccess ? JC_OK : hip_fail(W, e);
 }
@@ -1172,6 +1326,7 @@ int jc_ts_prep(jc_ctx* ctx, const float* window, const uint8_t* observed, int ro
         return fail(JC_EINVAL, "%s: sizes (rows=%d w=%d patch=%d; 1 <= patch <= 64 dividing w)", W, rows, w, patch);
     if ((int64_t)rows * w == 0) return JC_OK;
     if (!window || !observed || !tokens || !loc || !scale) return fail(JC_EINVAL, "%s: null buffer", W);
+    ProfScope ps(ctx, "ts prep");
     hipError_t e = jc::ts_prep_launch(window, observed, rows, w, patch, known, minimum_scale, use_asinh, tokens, scaled,
                                       loc, scale, ctx->stream);
     return e == hipSuccess ? JC_OK : hip_fail(W, e);
@@ -1190,6 +1345,7 @@ int jc_ts_finish(jc_ctx* ctx, const float* raw, const float* loc, const float* s
         return fail(JC_EINVAL, "%s: context_patches=%d * patch=%d exceeds the window w=%d", W, context_patches, patch, w);
     if (rows == 0) return JC_OK;
     if (!raw || !loc || !scale || !out || !width) return fail(JC_EINVAL, "%s: null buffer", W);
+    ProfScope ps(ctx, "ts finish");
     hipError_t e = jc::ts_finish_launch(raw, loc, scale, rows, w, (context_patches - 1) * patch, h * patch, q, width,
                                         median, use_asinh, out, ctx->stream);
     return e == hipSuccess ? JC_OK : hip_fail(W, e);

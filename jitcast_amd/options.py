@@ -11,6 +11,8 @@ Properties read by this package:
                             f16x3 keeps fp32 results with the GEMMs on three-term fp16 splits (f32)
   chronos2.hip.plans        plans cached per engine, one hipGraph per batch shape; 0 runs eagerly (8)
   chronos2.hip.planBytes    device bytes the cached plans may hold (the device's memory)
+  chronos2.hip.profile      print per-kernel times of each eager forward and the time of each plan
+                            replay to stderr, as -Dchronos2.tornado.profile (false)
   timestral.maxTokens       tokens (rows x patches) per Timestral forward pass before the pipeline
                             splits a call into windows (131072)
   timestral.hip.dtype       f32 | bf16 | fp16 | f16x3: the Timestral engine's GEMM and attention type (f32;
@@ -19,6 +21,7 @@ Properties read by this package:
   timestral.hip.plans       plans cached per HipTimestralModel, one hipGraph per block shape; 0 runs
                             eagerly (8)
   timestral.hip.planBytes   device bytes those plans may hold (the device's memory)
+  timestral.hip.profile     as chronos2.hip.profile, for the Timestral block (false)
   jitcast.hip.device        the GPU an engine runs on (0)
 """
 from __future__ import annotations

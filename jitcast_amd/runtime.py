@@ -6,7 +6,9 @@ runs in libjitcast_hip.
 from __future__ import annotations
 
 import ctypes
+import sys
 import threading
+from contextlib import contextmanager
 
 from . import _lib
 
@@ -29,6 +31,16 @@ class HipContext:
 
     def sync(self) -> None:
         _lib.call("jc_sync", self.handle)
+
+    def profile(self, on: bool) -> None:
+        """Starts (or restarts) or stops per-kernel timing on this context (jc_profile)."""
+        _lib.call("jc_profile", self.handle, 1 if on else 0)
+
+    def profile_report(self) -> str:
+        """The kernels timed since profiling started or the last report, one line each (jc_profile_report)."""
+        buf = ctypes.create_string_buffer(1 << 16)
+        _lib.call("jc_profile_report", self.handle, buf, len(buf))
+        return buf.value.decode()
 
     def device_info(self) -> tuple[int, str]:
         cus = ctypes.c_int()
@@ -71,6 +83,43 @@ def context(device: int = 0) -> HipContext:
         ctx = ctxs[device] = HipContext(device)
     ctx.bind_torch_stream()
     return ctx
+
+
+@contextmanager
+def kernel_profile(device: int, label: str, on: bool):
+    """Per-kernel times of the launches made inside the block, printed to stderr after it: the
+    counterpart of the reference's -D<model>.tornado.profile console profiler
+    (J/chronos2/tornado/Chronos2Forward.java:301-303). Does nothing when off, or while the current
+    stream is being captured into a plan (a capture records no events)."""
+    import torch
+
+    if not on or torch.cuda.is_current_stream_capturing():
+        yield
+        return
+    ctx = context(device)
+    ctx.profile(True)
+    try:
+        yield
+        report = context(device).profile_report()
+        print(f"[{label}]\n{report}", file=sys.stderr, end="", flush=True)
+    finally:
+        ctx.profile(False)
+
+
+def timed_replay(label: str, on: bool, replay) -> None:
+    """Runs replay(); when on, times it with HIP events on the current stream and prints the time to
+    stderr (a captured plan replays as one graph, so its kernels are not timed one by one)."""
+    if not on:
+        replay()
+        return
+    import torch
+
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    replay()
+    b.record()
+    b.synchronize()
+    print(f"[{label}] plan replay {a.elapsed_time(b):.4f} ms", file=sys.stderr, flush=True)
 
 
 def fill_normal(t, stream_seed: int, mean: float = 0.0, std: float = 1.0) -> None:

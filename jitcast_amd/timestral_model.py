@@ -31,7 +31,7 @@ from dataclasses import dataclass
 
 import numpy as np
 
-from . import _lib, chronos2, chronos2_model, timestral
+from . import _lib, chronos2, chronos2_model, runtime, timestral
 from . import options as opts
 from . import plans as plans_mod
 
@@ -165,6 +165,8 @@ class HipTimestralModel:
                        for lw in weights["layers"]]
         self._bufs = {}
         self.buckets = opts.boolean("timestral.hip.buckets", True) if buckets is None else bool(buckets)
+        # -Dtimestral.hip.profile: per-kernel times of each eager forward, the time of each plan replay
+        self.profile = opts.boolean("timestral.hip.profile", False)
         self.plans = None
         if max_plans is None:
             max_plans = opts.integer("timestral.hip.plans", 8, 0)
@@ -217,6 +219,13 @@ class HipTimestralModel:
         [rows*(enc+h)] table rows from jc_ts_block_layout, group_start / group_end [rows] and role
         [rows] (or None) as int32 device tensors; rows of a series contiguous. bufs: a plan's buffers
         (default: the eager forward's)."""
+        with runtime.kernel_profile(self.dev.index or 0, f"timestral.hip.profile forward rows={rows} n={enc + h}",
+                                    self.profile):
+            return self._forward_raw(tokens, key_valid, known, pos, group_start, group_end, role, covariates, rows,
+                                     enc, h, bufs)
+
+    def _forward_raw(self, tokens, key_valid, known, pos, group_start, group_end, role, covariates: bool, rows: int,
+                     enc: int, h: int, bufs):
         c = self.c
         n, d = enc + h, c.d_model
         b = bufs if bufs is not None else self._buffers(rows, enc, h)
@@ -402,7 +411,7 @@ class HipTimestralModel:
             b["ge"].copy_(ge)
             if role is not None:
                 b["role"].copy_(role)
-            plan.graph.launch()
+            runtime.timed_replay(f"timestral.hip.profile shape={shape}", self.profile, plan.graph.launch)
             return b["raw"]
 
         return self.plans.run(shape, self._capture, use)
