@@ -660,6 +660,10 @@ def main() -> int:
                     help="which workloads to run (profiling runs select one kernel)")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="only run 5 plain device copies of this many bytes (calibrates rocprof byte counters)")
+    ap.add_argument("--read-bytes", type=int, default=0,
+                    help="only run 5 sums over this many bytes of fp32 (a read stream: calibrates FETCH_SIZE)")
+    ap.add_argument("--write-bytes", type=int, default=0,
+                    help="only run 5 fills of this many bytes of fp32 (a write stream: calibrates WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (each series and each "
@@ -681,6 +685,21 @@ def main() -> int:
             b.copy_(a)
         torch.cuda.synchronize()
         log(f"copied {args.copy_bytes} bytes 5 times")
+        return 0
+    if args.read_bytes:
+        a = torch.empty(args.read_bytes // 4, dtype=torch.float32, device=dev).fill_(1.0)
+        torch.cuda.synchronize()
+        total = [a.sum() for _ in range(5)]
+        torch.cuda.synchronize()
+        log(f"summed {args.read_bytes} bytes 5 times ({float(total[-1]):.0f})")
+        return 0
+    if args.write_bytes:
+        a = torch.empty(args.write_bytes // 4, dtype=torch.float32, device=dev)
+        torch.cuda.synchronize()
+        for v in range(5):
+            a.fill_(float(v))
+        torch.cuda.synchronize()
+        log(f"filled {args.write_bytes} bytes 5 times")
         return 0
     also = {}
     want_cpu = not args.no_cpu_baseline

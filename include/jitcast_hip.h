@@ -171,8 +171,9 @@ int jc_c2_time_attention(jc_ctx *ctx, const void *qkv, void *out, const int32_t 
  * dh, inner) (J/chronos2/tornado/Chronos2Kernels.java:473-474), oracle CpuChronos2.java:230-282.
  *   qkv, out     device, as jc_c2_time_attention (the group sublayer's own projection)
  *   group_start  device int32 [rows]; group_end device int32 [rows] (jc_c2_group_bounds)
- *   dh           a multiple of 8, at most 64 (the reference takes multiples of 16); fp32 only
- *                (bf16/fp16 return JC_EUNSUPPORTED)
+ *   dh           a multiple of 8, at most 64 (the reference takes multiples of 16)
+ *   dtype        the storage type of qkv and out: JC_F32, or JC_BF16 / JC_F16 (values widened to
+ *                fp32 at load, scores, softmax and accumulation in fp32, out rounded once)
  */
 int jc_c2_group_attention(jc_ctx *ctx, const void *qkv, void *out, const int32_t *live, const int32_t *group_start,
                           const int32_t *group_end, int rows, int n, int heads, int dh, int inner, int dtype);
@@ -233,7 +234,8 @@ int jc_ts_gate(jc_ctx *ctx, void *att, const void *g, int64_t count, int dtype);
  * masks BlockLayout.java:223-243.
  *   key_valid  device int32 [rows*enc]; role device int32 [rows] (0 TARGET, 1 PAST, 2 KNOWN;
  *              BlockInput.java:35-37), may be NULL when covariates == 0
- *   gate       device fp32 [rows*n, d] or NULL; dtype: JC_F32 (bf16/fp16 return JC_EUNSUPPORTED)
+ *   gate       device [rows*n, d] of `dtype` or NULL; dtype: the storage type of qkv, gate and out,
+ *              JC_F32 or JC_BF16 / JC_F16 (fp32 arithmetic, out rounded once)
  *   dh         a multiple of 8, at most 128; d >= heads*dh
  */
 int jc_ts_variate_attention(jc_ctx *ctx, const void *qkv, void *out, const int32_t *key_valid,
@@ -367,7 +369,8 @@ typedef struct jc_c2_layer_weights {
 /* Bytes of the workspace jc_c2_layer needs for T = rows*n tokens, each part 256-byte aligned, or
  * -1 for a negative size. JC_F32: hn [T, d], big [T, max(3*inner, dff)], att [T, inner] floats.
  * JC_BF16 / JC_F16: hn [T, d] and att [T, inner] in the storage type, big [T, max(3*inner floats,
- * dff storage values)] and an fp32 att [T, inner] for the group attention. JC_F16X3: big
+ * dff storage values)] and an fp32 [T, inner] part the layer no longer uses (the size stays as it
+ * was, so callers' workspaces keep fitting). JC_F16X3: big
  * [T, max(3*inner, dff)] and att [T, inner] floats and the split operand [T, 3*max(d, inner, dff)]
  * fp16. */
 int64_t jc_c2_layer_workspace_bytes(int rows, int n, int d, int inner, int dff, int dtype);
@@ -384,9 +387,9 @@ int64_t jc_c2_layer_workspace_bytes(int rows, int n, int d, int inner, int dff, 
  * jc_c2_layer_workspace_bytes, 256-byte aligned. inner = heads*dh. d a multiple of 16, dh a multiple
  * of 16 and at most 64, dff a multiple of 16.
  * dtype JC_F32: everything in fp32. JC_BF16 / JC_F16: the GEMMs take the storage type with fp32
- * accumulation (the reference's FP16 GEMM modes, Chronos2Forward.java:377-409, GemmMode.HALF), the
- * time attention runs in the storage type, the group attention in fp32, and x (the residual
- * stream), the norms and the accumulations stay fp32. JC_F16X3 (no reference counterpart): every
+ * accumulation (the reference's FP16 GEMM modes, Chronos2Forward.java:377-409, GemmMode.HALF), both
+ * attention cores read q|k|v and write their output in the storage type (fp32 arithmetic inside),
+ * and x (the residual stream), the norms and the accumulations stay fp32. JC_F16X3 (no reference counterpart): every
  * GEMM runs on its operands' three-term fp16 splits (jc_split_f16x3; the norms, and the attention
  * kernels for 64-wide heads, write the split directly), with fp32 accumulation and fp32 outputs;
  * the attention, the norms and x are fp32, as in JC_F32, whose accuracy it keeps to about 2^-20 per

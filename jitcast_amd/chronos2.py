@@ -61,7 +61,8 @@ def group_attention(qkv, out, live, group_start, group_end, rows: int, n: int, h
                     inner: int) -> None:
     """Attention across the rows of each group at every slot (Chronos2Kernels.groupAttention).
 
-    group_start/group_end: int32 [rows] device tensors (see group_bounds); groups contiguous.
+    qkv [rows*n, 3*inner] and out [rows*n, inner] float32, bfloat16 or float16 (both the same; fp32
+    arithmetic); group_start/group_end: int32 [rows] device tensors (see group_bounds); groups contiguous.
     """
     dt = _dtype_code(qkv)
     if _dtype_code(out) != dt:

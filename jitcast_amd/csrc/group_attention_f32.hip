@@ -13,6 +13,10 @@
 // patch is a valid key; with covariates a covariate row never reads a target row and a known row
 // reads only known rows; a row always reads itself. The optional sigmoid gate is fused.
 //
+// Storage types: q|k|v, the gate and out are fp32, or (T = bf16 / fp16, the layers' FP16 GEMM mode)
+// 16-bit values widened to fp32 at load and rounded once at the store; scores, softmax and
+// accumulation are fp32 either way.
+//
 // The stage reads q|k|v once and writes out once, about 10 flop per byte: it is HBM-bound, so the
 // kernel is built around the memory stream. One wave per (16-row tile, slot) owns the groups that
 // START in its tile (found by a ballot on groupStart[i] == i), so each row's q, k and v are fetched
@@ -31,14 +35,39 @@
 //                        per lane as V[key][e] (16 rows x 64 contiguous bytes per load).
 #include <algorithm>
 #include <cstdlib>
+#include <type_traits>
 
 #include "jc_common.hpp"
 #include "jc_kernels.hpp"
+#include "lp_common.hpp"
 
 namespace jc {
 namespace {
 
 constexpr int kRT = 16;  // rows per tile (queries and keys)
+
+// four consecutive storage values as fp32 (one 16- or 8-byte load), and back
+template <typename T>
+__device__ __forceinline__ floatx4 load4(const T* p) {
+    if constexpr (std::is_same_v<T, float>) {
+        return *reinterpret_cast<const floatx4*>(p);
+    } else {
+        typedef T t4 __attribute__((ext_vector_type(4)));
+        const t4 v = __builtin_bit_cast(t4, *reinterpret_cast<const lp::u32x2*>(p));
+        floatx4 r;
+#pragma unroll
+        for (int u = 0; u < 4; u++) r[u] = (float)v[u];
+        return r;
+    }
+}
+template <typename T>
+__device__ __forceinline__ void store4(T* p, floatx4 v) {
+    if constexpr (std::is_same_v<T, float>) {
+        *reinterpret_cast<floatx4*>(p) = v;
+    } else {
+        *reinterpret_cast<lp::u32x2*>(p) = lp::narrow4<T>(v);
+    }
+}
 
 // max / sum over the four lanes j, j+16, j+32, j+48 (v_permlane16_swap then v_permlane32_swap)
 __device__ __forceinline__ float quad_max(float v) {
@@ -64,14 +93,18 @@ struct Job {
 
 // X3 (Chronos-2, 64-wide heads; the JC_F16X3 layer): out holds fp16 rows of 3 * inner values, the
 // O projection's A operand [hi | hi | lo] (the three-term split of each fp32 output value).
-template <int DHP, bool TS, bool EXACT, bool X3>
+// T: the storage type of q|k|v, the gate and out (float, __bf16 or _Float16).
+template <typename T, int DHP, bool TS, bool EXACT, bool X3>
 __global__ __launch_bounds__(kWave) void group_attention_f32(const GroupArgs a, int dh_rt) {
-    static_assert(!X3 || (!TS && EXACT && DHP == 64), "split output: Chronos-2, 64-wide heads");
+    static_assert(!X3 || (!TS && EXACT && DHP == 64 && std::is_same_v<T, float>),
+                  "split output: Chronos-2, 64-wide heads, fp32");
     static_assert(DHP % 16 == 0 && DHP <= 128, "head width");
     constexpr int kM = DHP / 16;            // 16-dim groups: K/Q loads per lane, and output dim tiles
     constexpr int kQT = DHP <= 64 ? 4 : 2;  // query tiles held in registers at once
     const int dh = EXACT ? DHP : dh_rt;
-    const float* __restrict__ qkv = a.qkv;
+    const T* __restrict__ qkv = static_cast<const T*>(a.qkv);
+    const T* __restrict__ gate = static_cast<const T*>(a.gate);
+    T* __restrict__ out = static_cast<T*>(a.out);
     const int rows = a.rows, n = a.n, heads = a.heads, inner = a.inner;
     const int lane = threadIdx.x;
     const int j = lane % 16, g = lane / 16;
@@ -107,11 +140,11 @@ __global__ __launch_bounds__(kWave) void group_attention_f32(const GroupArgs a, 
         const int hn = h_hi - h_lo;
         for (int pr = lane / 16; pr < nr * hn; pr += kWave / 16) {
             const int row = r0 + pr / hn, h = h_lo + pr % hn;
-            const float* tokp = qkv + ((size_t)row * tok_n + t) * stride + h * dh;
+            const T* tokp = qkv + ((size_t)row * tok_n + t) * stride + h * dh;
             float sc = 0.f;
             for (int e = 4 * pj; e < dh; e += 64) {
-                const floatx4 q4 = *reinterpret_cast<const floatx4*>(tokp + e);
-                const floatx4 k4 = *reinterpret_cast<const floatx4*>(tokp + inner + e);
+                const floatx4 q4 = load4(tokp + e);
+                const floatx4 k4 = load4(tokp + inner + e);
 #pragma unroll
                 for (int u = 0; u < 4; u++) sc += (q4[u] * a.qscale) * k4[u];
             }
@@ -122,19 +155,19 @@ __global__ __launch_bounds__(kWave) void group_attention_f32(const GroupArgs a, 
             const bool nan = !zero && !(sc < INFINITY);  // NaN or +inf
             const size_t off = ((size_t)row * tok_n + t) * inner + h * dh;
             for (int e = 4 * pj; e < dh; e += 64) {
-                floatx4 v = *reinterpret_cast<const floatx4*>(tokp + 2 * inner + e);
+                floatx4 v = load4(tokp + 2 * inner + e);
 #pragma unroll
                 for (int u = 0; u < 4; u++) v[u] = zero ? 0.f : nan ? __builtin_nanf("") : v[u];
-                if (a.gate) {
-                    const floatx4 gv = *reinterpret_cast<const floatx4*>(a.gate + off + e);
+                if (gate) {
+                    const floatx4 gv = load4(gate + off + e);
 #pragma unroll
                     for (int u = 0; u < 4; u++) v[u] *= 1.f / (1.f + fast_exp2(-gv[u] * kLog2e));
                 }
                 if constexpr (X3) {
-                    store_split_row(reinterpret_cast<_Float16*>(a.out) + ((size_t)row * tok_n + t) * 3 * inner, inner,
+                    store_split_row(static_cast<_Float16*>(a.out) + ((size_t)row * tok_n + t) * 3 * inner, inner,
                                     h * dh + e, v);
                 } else {
-                    *reinterpret_cast<floatx4*>(a.out + off + e) = v;
+                    store4(out + off + e, v);
                 }
             }
         }
@@ -176,7 +209,7 @@ __global__ __launch_bounds__(kWave) void group_attention_f32(const GroupArgs a, 
     auto load_kv = [&](const Job& jb, Kv& d) {
         const int kbase = jb.gs + kRT * jb.kt;
         const int krow = min(kbase + j, jb.ge - 1);
-        const float* kp = qkv + ((size_t)krow * tok_n + t) * stride + inner + jb.h * dh + 4 * g;
+        const T* kp = qkv + ((size_t)krow * tok_n + t) * stride + inner + jb.h * dh + 4 * g;
         const bool in_group = g == 0 && kbase + j < jb.ge;
         if (TS) {
             d.valid = in_group && (!enc_slot || a.valid[(size_t)krow * a.enc + t] != 0);
@@ -187,14 +220,13 @@ __global__ __launch_bounds__(kWave) void group_attention_f32(const GroupArgs a, 
         }
 #pragma unroll
         for (int m = 0; m < kM; m++)
-            d.k[m] = (EXACT || 16 * m + 4 * g < dh) ? *reinterpret_cast<const floatx4*>(kp + 16 * m)
-                                                     : floatx4{0.f, 0.f, 0.f, 0.f};
+            d.k[m] = (EXACT || 16 * m + 4 * g < dh) ? load4(kp + 16 * m) : floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int c = 0; c < 4; c++) {
             const int vrow = min(kbase + 4 * g + c, jb.ge - 1);
-            const float* vp = qkv + ((size_t)vrow * tok_n + t) * stride + 2 * inner + jb.h * dh + j;
+            const T* vp = qkv + ((size_t)vrow * tok_n + t) * stride + 2 * inner + jb.h * dh + j;
 #pragma unroll
-            for (int m = 0; m < kM; m++) d.v[m][c] = (EXACT || 16 * m + j < dh) ? vp[16 * m] : 0.f;
+            for (int m = 0; m < kM; m++) d.v[m][c] = (EXACT || 16 * m + j < dh) ? (float)vp[16 * m] : 0.f;
         }
     };
 
@@ -215,11 +247,10 @@ __global__ __launch_bounds__(kWave) void group_attention_f32(const GroupArgs a, 
             for (int qi = 0; qi < kQT; qi++) {
                 if (qi < nq) {
                     const int qrow = min(cur.gs + kRT * (kQT * cur.qc + qi) + j, cur.ge - 1);
-                    const float* qp = qkv + ((size_t)qrow * tok_n + t) * stride + cur.h * dh + 4 * g;
+                    const T* qp = qkv + ((size_t)qrow * tok_n + t) * stride + cur.h * dh + 4 * g;
 #pragma unroll
                     for (int m = 0; m < kM; m++) {
-                        floatx4 x = (EXACT || 16 * m + 4 * g < dh) ? *reinterpret_cast<const floatx4*>(qp + 16 * m)
-                                                                    : floatx4{0.f, 0.f, 0.f, 0.f};
+                        floatx4 x = (EXACT || 16 * m + 4 * g < dh) ? load4(qp + 16 * m) : floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                         for (int u = 0; u < 4; u++) qreg[qi][4 * m + u] = x[u] * a.qscale;
                     }
@@ -302,18 +333,18 @@ __global__ __launch_bounds__(kWave) void group_attention_f32(const GroupArgs a, 
                         for (int m = 0; m < kM; m++) {
                             if (EXACT || 16 * m + 4 * g < dh) {
                                 floatx4 v = o_acc[qi][m] * inv;
-                                if (a.gate) {
+                                if (gate) {
                                     // the output gate: att * sigmoid(g) (CpuTimestral.java:156-161)
-                                    const floatx4 gv = *reinterpret_cast<const floatx4*>(a.gate + off + 16 * m);
+                                    const floatx4 gv = load4(gate + off + 16 * m);
 #pragma unroll
                                     for (int u = 0; u < 4; u++) v[u] *= 1.f / (1.f + fast_exp2(-gv[u] * kLog2e));
                                 }
                                 if constexpr (X3) {
                                     store_split_row(
-                                        reinterpret_cast<_Float16*>(a.out) + ((size_t)qrow * tok_n + t) * 3 * inner,
+                                        static_cast<_Float16*>(a.out) + ((size_t)qrow * tok_n + t) * 3 * inner,
                                         inner, cur.h * dh + 4 * g + 16 * m, v);
                                 } else {
-                                    *reinterpret_cast<floatx4*>(a.out + off + 16 * m) = v;
+                                    store4(out + off + 16 * m, v);
                                 }
                             }
                         }
@@ -339,40 +370,50 @@ static int group_head_split() {
     return v >= 1 && v <= 16 ? v : 4;
 }
 
-template <int DHP, bool TS, bool EXACT, bool X3 = false>
+template <typename T, int DHP, bool TS, bool EXACT, bool X3 = false>
 static hipError_t launch_group(GroupArgs a, int dh, hipStream_t stream) {
     a.rtiles = (a.rows + kRT - 1) / kRT;
     a.hsplit = std::min(group_head_split(), a.heads);
     const uint64_t grid = (uint64_t)a.rtiles * a.n * a.hsplit;
     if (grid > 0xffffffffull) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((group_attention_f32<DHP, TS, EXACT, X3>), dim3((uint32_t)grid), dim3(kWave), 0, stream, a,
+    hipLaunchKernelGGL((group_attention_f32<T, DHP, TS, EXACT, X3>), dim3((uint32_t)grid), dim3(kWave), 0, stream, a,
                        dh);
     return hipGetLastError();
 }
 
-template <int DHP, bool TS>
+template <typename T, int DHP, bool TS>
 static hipError_t launch_group_width(const GroupArgs& a, int dh, hipStream_t stream) {
-    return dh == DHP ? launch_group<DHP, TS, true>(a, dh, stream) : launch_group<DHP, TS, false>(a, dh, stream);
+    return dh == DHP ? launch_group<T, DHP, TS, true>(a, dh, stream) : launch_group<T, DHP, TS, false>(a, dh, stream);
 }
 
-template <bool TS>
+template <typename T, bool TS>
 static hipError_t dispatch_group(const GroupArgs& a, int dh, hipStream_t stream) {
-    if (dh <= 16) return launch_group_width<16, TS>(a, dh, stream);
-    if (dh <= 32) return launch_group_width<32, TS>(a, dh, stream);
-    if (dh == 48) return launch_group<48, TS, true>(a, dh, stream);
-    if (dh <= 64 || !TS) return launch_group_width<64, TS>(a, dh, stream);
-    if constexpr (TS) return launch_group_width<128, TS>(a, dh, stream);  // Chronos-2 heads are at most 64 wide
+    if (dh <= 16) return launch_group_width<T, 16, TS>(a, dh, stream);
+    if (dh <= 32) return launch_group_width<T, 32, TS>(a, dh, stream);
+    if (dh == 48) return launch_group<T, 48, TS, true>(a, dh, stream);
+    if (dh <= 64 || !TS) return launch_group_width<T, 64, TS>(a, dh, stream);
+    if constexpr (TS) return launch_group_width<T, 128, TS>(a, dh, stream);  // Chronos-2 heads are at most 64 wide
     return hipErrorInvalidValue;
 }
 
-hipError_t group_attention_f32_launch(const GroupArgs& a, int dh, bool ts, hipStream_t stream) {
+template <typename T>
+static hipError_t dispatch_group_type(const GroupArgs& a, int dh, bool ts, hipStream_t stream) {
+    return ts ? dispatch_group<T, true>(a, dh, stream) : dispatch_group<T, false>(a, dh, stream);
+}
+
+hipError_t group_attention_launch(const GroupArgs& a, int dh, bool ts, int dtype, hipStream_t stream) {
     if (dh < 8 || dh > 128 || dh % 8) return hipErrorInvalidValue;
-    return ts ? dispatch_group<true>(a, dh, stream) : dispatch_group<false>(a, dh, stream);
+    switch (dtype) {  // the jc_dtype codes: 0 fp32, 1 bf16, 2 fp16
+        case 0: return dispatch_group_type<float>(a, dh, ts, stream);
+        case 1: return dispatch_group_type<__bf16>(a, dh, ts, stream);
+        case 2: return dispatch_group_type<_Float16>(a, dh, ts, stream);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 hipError_t group_attention_f32_x3_launch(const GroupArgs& a, int dh, hipStream_t stream) {
     if (dh != 64) return hipErrorInvalidValue;
-    return launch_group<64, false, true, true>(a, dh, stream);
+    return launch_group<float, 64, false, true, true>(a, dh, stream);
 }
 
 }  // namespace jc

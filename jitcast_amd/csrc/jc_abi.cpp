@@ -594,7 +594,6 @@ static int check_group_common(const char* W, const void* qkv, const void* out, c
     if (inner < heads * dh || inner % 4)
         return fail(JC_EINVAL, "%s: inner %d (need >= heads*dh = %d and a multiple of 4)", W, inner, heads * dh);
     if (dtype != JC_F32 && dtype != JC_BF16 && dtype != JC_F16) return fail(JC_EINVAL, "%s: dtype %d", W, dtype);
-    if (dtype != JC_F32) return fail(JC_EUNSUPPORTED, "%s: dtype %d is not built yet (fp32 only)", W, dtype);
     if ((size_t)rows * n == 0) return JC_OK;
     if (!qkv || !out || !gs || !ge) return fail(JC_EINVAL, "%s: null device pointer", W);
     if (!aligned16(qkv) || !aligned16(out) || (gate && !aligned16(gate)))
@@ -610,9 +609,10 @@ static int c2_group(jc_ctx* ctx, const char* W, const void* qkv, void* out, cons
     int rc = check_group_common(W, qkv, out, nullptr, group_start, group_end, rows, n, heads, dh, inner, dtype, 64);
     if (rc || (size_t)rows * n == 0) return rc;
     if (!live) return fail(JC_EINVAL, "%s: null live mask", W);
+    if (x3 && dtype != JC_F32) return fail(JC_EINVAL, "%s: the split output needs fp32", W);
     jc::GroupArgs a{};
-    a.qkv = (const float*)qkv;
-    a.out = (float*)out;
+    a.qkv = qkv;
+    a.out = out;
     a.valid = live;
     a.gstart = group_start;
     a.gend = group_end;
@@ -622,9 +622,9 @@ static int c2_group(jc_ctx* ctx, const char* W, const void* qkv, void* out, cons
     a.inner = inner;
     a.enc = n;
     a.qscale = 1.4426950408889634f;  // unscaled scores, exp via exp2
-    ProfScope ps(ctx, x3 ? "c2 group_attention_f32 (split out)" : "c2 group_attention_f32");
+    ProfScope ps(ctx, x3 ? "c2 group_attention (split out)" : dtype == JC_F32 ? "c2 group_attention_f32" : "c2 group_attention_lp");
     hipError_t e = x3 ? jc::group_attention_f32_x3_launch(a, dh, ctx->stream)
-                      : jc::group_attention_f32_launch(a, dh, false, ctx->stream);
+                      : jc::group_attention_launch(a, dh, false, dtype, ctx->stream);
     return e == hipSuccess ? JC_OK : hip_fail(W, e);
 }
 
@@ -648,13 +648,13 @@ int jc_ts_variate_attention(jc_ctx* ctx, const void* qkv, void* out, const int32
     if (enc > 0 && !key_valid) return fail(JC_EINVAL, "%s: null key_valid", W);
     if (covariates && !role) return fail(JC_EINVAL, "%s: covariates without a role array", W);
     jc::GroupArgs a{};
-    a.qkv = (const float*)qkv;
-    a.out = (float*)out;
+    a.qkv = qkv;
+    a.out = out;
     a.valid = key_valid;
     a.gstart = group_start;
     a.gend = group_end;
     a.role = role;
-    a.gate = (const float*)gate;
+    a.gate = gate;
     a.rows = rows;
     a.n = n;
     a.heads = heads;
@@ -662,8 +662,8 @@ int jc_ts_variate_attention(jc_ctx* ctx, const void* qkv, void* out, const int32
     a.enc = enc;
     a.covariates = covariates;
     a.qscale = (float)(1.4426950408889634 / std::sqrt((double)dh));
-    ProfScope ps(ctx, "ts variate_attention_f32");
-    hipError_t e = jc::group_attention_f32_launch(a, dh, true, ctx->stream);
+    ProfScope ps(ctx, dtype == JC_F32 ? "ts variate_attention_f32" : "ts variate_attention_lp");
+    hipError_t e = jc::group_attention_launch(a, dh, true, dtype, ctx->stream);
     return e == hipSuccess ? JC_OK : hip_fail(W, e);
 }
 
@@ -1055,7 +1055,6 @@ static int layer_lp(jc_ctx* ctx, const char* W, float* x, const jc_c2_layer_weig
     char* ws = static_cast<char*>(workspace);
     void* hn = ws;                                                   // [T, d] storage type
     void* big = ws + round256(t * d * 2);                            // qkv [T, 3*inner] (storage type or fp32) or act [T, dff]
-    float* att32 = reinterpret_cast<float*>(ws + round256(t * d * 2) + round256(t * big_bytes));  // [T, inner] fp32
     void* att = ws + round256(t * d * 2) + round256(t * big_bytes) + round256(t * (size_t)inner * 4);  // [T, inner]
     int rc;
     // time attention sub-layer (Chronos2Forward.java:260-271), qkv and att in the storage type
@@ -1067,15 +1066,13 @@ static int layer_lp(jc_ctx* ctx, const char* W, float* x, const jc_c2_layer_weig
     if ((rc = launch_linear_lp(ctx, W, att, inner, w->time_o, w->time_o_bias, x, d, T, d, inner, JC_GEMM_ACCUMULATE,
                                dtype, JC_F32)))
         return rc;
-    // group attention sub-layer (Chronos2Forward.java:273-281): the group attention is fp32, so its
-    // qkv comes out of the GEMM in fp32 and its output is rounded once for the O projection
+    // group attention sub-layer (Chronos2Forward.java:273-281), qkv and att in the storage type
     if ((rc = launch_rms_lp(ctx, W, x, w->group_norm, hn, T, d, eps, dtype))) return rc;
     if ((rc = launch_linear_lp(ctx, W, hn, d, w->group_qkv, w->group_qkv_bias, big, 3 * inner, T, 3 * inner, d, 0,
-                               dtype, JC_F32)))
+                               dtype, dtype)))
         return rc;
-    if ((rc = jc_c2_group_attention(ctx, big, att32, live, group_start, group_end, rows, n, heads, dh, inner, JC_F32)))
+    if ((rc = jc_c2_group_attention(ctx, big, att, live, group_start, group_end, rows, n, heads, dh, inner, dtype)))
         return rc;
-    if ((rc = launch_to_lp(ctx, W, att32, att, (int64_t)t * inner, dtype))) return rc;
     if ((rc = launch_linear_lp(ctx, W, att, inner, w->group_o, w->group_o_bias, x, d, T, d, inner, JC_GEMM_ACCUMULATE,
                                dtype, JC_F32)))
         return rc;

@@ -29,13 +29,13 @@ hipError_t time_attention_lpp_launch(const TimeArgs& a, bool fp16, int cus, hipS
 hipError_t gate_launch(void* att, const void* g, uint64_t count, int dtype, hipStream_t stream);
 // The arguments of the group-attention kernels (by value).
 struct GroupArgs {
-    const float* qkv;       // [rows*n, 3*inner]
-    float* out;             // [rows*n, inner]
+    const void* qkv;        // [rows*n, 3*inner] of the storage type
+    void* out;              // [rows*n, inner] of the storage type
     const int32_t* valid;   // Chronos-2: live [rows*n]; Timestral: keyValid [rows*enc]
     const int32_t* gstart;  // [rows]
     const int32_t* gend;    // [rows]
     const int32_t* role;    // Timestral: [rows] TARGET 0 / PAST 1 / KNOWN 2, or null
-    const float* gate;      // [rows*n, inner]: out *= sigmoid(gate); or null
+    const void* gate;       // [rows*n, inner] of the storage type: out *= sigmoid(gate); or null
     int rows, n, heads, inner;
     int enc;                // Timestral's encoder slots (keyValid applies to t < enc)
     int covariates;         // Timestral: whether the block runs the covariate rules
@@ -45,8 +45,9 @@ struct GroupArgs {
 };
 
 // Chronos-2 group attention (ts = false) or Timestral variate attention (ts = true); a.rtiles is
-// set by the launcher. dh a multiple of 8, at most 128 (64 for Chronos-2).
-hipError_t group_attention_f32_launch(const GroupArgs& a, int dh, bool ts, hipStream_t stream);
+// set by the launcher. dh a multiple of 8, at most 128 (64 for Chronos-2). dtype (0 fp32, 1 bf16,
+// 2 fp16) is the storage type of qkv, the gate and out; the arithmetic is fp32.
+hipError_t group_attention_launch(const GroupArgs& a, int dh, bool ts, int dtype, hipStream_t stream);
 // Chronos-2 with 64-wide heads only (else hipErrorInvalidValue): a.out is read as fp16 [rows*n, 3*inner],
 // each output value's three-term split [hi | hi | lo].
 hipError_t group_attention_f32_x3_launch(const GroupArgs& a, int dh, hipStream_t stream);

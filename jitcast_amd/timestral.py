@@ -49,7 +49,8 @@ def variate_attention(qkv, out, key_valid, group_start, group_end, role, covaria
     """Attention across the rows of each series per slot (TimestralKernels.variateAttention), scaled
     by 1/sqrt(dh), under BlockLayout.variateAllowed; out *= sigmoid(gate) when gate is given.
 
-    qkv [rows*n, 3*d] and out (and gate) [rows*n, d] float32; key_valid int32 [rows*enc];
+    qkv [rows*n, 3*d] and out (and gate) [rows*n, d] float32, bfloat16 or float16 (all the same; fp32
+    arithmetic); key_valid int32 [rows*enc];
     group_start/group_end int32 [rows] (contiguous groups); role int32 [rows] or None.
     """
     dt = _dtype_code(qkv)

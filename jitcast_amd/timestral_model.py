@@ -293,8 +293,8 @@ class HipTimestralModel:
         for lw in self.layers:
             for a in lw["attentions"]:
                 hn = norm(a["norm"])
-                # the time attention reads q|k|v and the gate in the storage type, the variate one in fp32
-                lp_att = lowp and a["time"]
+                # both attention cores read q|k|v and the gate in the storage type (fp32 arithmetic)
+                lp_att = lowp
                 qkv = view(b["big_lp"] if lp_att else b["big"], 3 * d)
                 att = b["att_lp"] if lp_att else b["att"]
                 gemm(hn, a["qkv"], qkv)
@@ -308,9 +308,6 @@ class HipTimestralModel:
                 else:
                     timestral.variate_attention(qkv, att, key_valid, group_start, group_end, role, covariates, g, rows,
                                                 enc, n, heads, dh, d)
-                if lowp and not a["time"]:
-                    chronos2.to_lp(att, b["att_lp"])
-                    att = b["att_lp"]
                 gemm(operand(att, d), a["wo"], x, chronos2.GEMM_ACCUMULATE)
             if not mlp:
                 continue

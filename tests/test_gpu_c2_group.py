@@ -1,5 +1,7 @@
-"""GPU parity of Chronos-2 group attention against the C oracle (through the C ABI). Bar: max
-relative error <= 1e-4 (fp32)."""
+"""GPU parity of Chronos-2 group attention against the C oracle (through the C ABI). Bars: max
+relative error <= 1e-4 (fp32). bf16 / fp16 storage (fp32 arithmetic, the output rounded once): against
+the oracle on the same rounded inputs within 2^-8 (bf16) / 2^-11 (fp16), the output's own rounding
+with room to spare, and against the oracle on the unrounded fp32 inputs within 2e-2."""
 import numpy as np
 import pytest
 import torch
@@ -9,6 +11,9 @@ from tests import cases
 
 pytestmark = pytest.mark.gpu
 TOL_F32 = 1e-4
+LP = {"bf16": torch.bfloat16, "fp16": torch.float16}
+TOL_ROUNDED = {"bf16": 2.0 ** -8, "fp16": 2.0 ** -11}
+TOL_LP = 2e-2
 
 
 def _run(qkv, live, group, rows, n, heads, dh, inner):
@@ -36,6 +41,36 @@ CASES = [
     (260, 3, 12, 64, 768, 260, 260, 0.9),  # one group of a whole batch (cross-learning): 5 query chunks
     (40, 2, 5, 64, 320, 1, 30, 0.8),  # 5 heads over 4 waves per tile: ranges of 1 and 2 heads
 ]
+
+
+def _run_lp(qkv, live, group, rows, n, heads, dh, inner, dt):
+    """The kernel on qkv rounded to the storage type: (the rounded qkv as fp32, the output as fp32)."""
+    dev = torch.device("cuda:0")
+    s, e = chronos2.group_bounds(group)
+    q = torch.from_numpy(qkv).to(dev).to(LP[dt])
+    out = torch.full((rows * n, inner), float("nan"), dtype=LP[dt], device=dev)
+    chronos2.group_attention(q, out, torch.from_numpy(np.ascontiguousarray(live.reshape(-1), np.int32)).to(dev),
+                             torch.from_numpy(s).to(dev), torch.from_numpy(e).to(dev), rows, n, heads, dh, inner)
+    torch.cuda.synchronize()
+    return q.float().cpu().numpy(), out.float().cpu().numpy()
+
+
+@pytest.mark.parametrize("dt", sorted(LP))
+@pytest.mark.parametrize("rows,n,heads,dh,inner,lo,hi,p", CASES)
+def test_lowp_matches_oracle(gpu, oracle, dt, rows, n, heads, dh, inner, lo, hi, p):
+    print(f"case {dt} rows={rows} n={n} heads={heads} dh={dh} groups {lo}..{hi} live {p}", flush=True)
+    qkv = cases.qkv(41, rows * n, inner)
+    live = cases.random_live(41, rows, n, p)
+    group = cases.group_sizes(41, rows, lo, hi)
+    qr, got = _run_lp(qkv, live, group, rows, n, heads, dh, inner, dt)
+    got = got[:, : heads * dh]
+    assert np.isfinite(got).all()
+    exp_r = oracle.c2_group_attention(qr, live, group, rows, n, heads, dh, inner)[:, : heads * dh]
+    exp = oracle.c2_group_attention(qkv, live, group, rows, n, heads, dh, inner)[:, : heads * dh]
+    err_r, err = oracle.rel_max_error(got, exp_r), oracle.rel_max_error(got, exp)
+    print(f"  rel err {err_r:.3e} on the rounded inputs, {err:.3e} against fp32", flush=True)
+    assert err_r <= TOL_ROUNDED[dt]
+    assert err <= TOL_LP
 
 
 @pytest.mark.parametrize("rows,n,heads,dh,inner,lo,hi,p", CASES)

@@ -4,7 +4,7 @@ import numpy as np
 import pytest
 import torch
 
-from jitcast_amd import JitcastError, chronos2, rng, timestral
+from jitcast_amd import chronos2, rng, timestral
 from tests import cases
 
 pytestmark = pytest.mark.gpu
@@ -90,13 +90,46 @@ def test_known_rows_never_read_other_rows(gpu, oracle):
     assert np.abs(pert[0] - base[0]).max() > 1e-3
 
 
-def test_bf16_is_not_built_yet(gpu):
+LP = {"bf16": torch.bfloat16, "fp16": torch.float16}
+
+
+@pytest.mark.parametrize("dt", sorted(LP))
+@pytest.mark.parametrize("rows,enc,h,heads,dh,d,lo,hi,cov,p,gate", CASES)
+def test_lowp_matches_oracle(gpu, oracle, dt, rows, enc, h, heads, dh, d, lo, hi, cov, p, gate):
+    """bf16 / fp16 storage of q|k|v, the gate and out, fp32 arithmetic: against the oracle on the same
+    rounded inputs within 2^-8 (bf16) / 2^-11 (fp16), and on the unrounded fp32 inputs within 2e-2."""
+    print(f"case {dt} rows={rows} enc={enc} h={h} heads={heads} dh={dh} groups {lo}..{hi} cov={cov} gate={gate}",
+          flush=True)
     dev = torch.device("cuda:0")
-    q = torch.zeros(4 * 3 * 64, dtype=torch.bfloat16, device=dev)
-    o = torch.zeros(4 * 64, dtype=torch.bfloat16, device=dev)
-    z = torch.zeros(4, dtype=torch.int32, device=dev)
-    with pytest.raises(JitcastError, match="not built"):
-        timestral.variate_attention(q, o, z, z, z + 1, None, False, None, 4, 1, 1, 1, 64, 64)
+    n = enc + h
+    qkv = cases.qkv(107, rows * n, d)
+    kv = cases.random_live(107, rows, max(enc, 1), p)[:, :enc].copy()
+    group = cases.group_sizes(107, rows, lo, hi)
+    role = _roles(107, rows) if cov else np.zeros(rows, np.int32)
+    g = cases.qkv(108, rows * n, d)[:, :d].copy() if gate else None
+    s, e = chronos2.group_bounds(group)
+
+    def i32(a):
+        return torch.from_numpy(np.ascontiguousarray(a, np.int32).reshape(-1)).to(dev)
+
+    q = torch.from_numpy(qkv).to(dev).to(LP[dt])
+    gt = torch.from_numpy(g).to(dev).to(LP[dt]) if g is not None else None
+    out = torch.full((rows * n, d), float("nan"), dtype=LP[dt], device=dev)
+    timestral.variate_attention(q, out, i32(kv), i32(s), i32(e), i32(role), cov, gt, rows, enc, n, heads, dh, d)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()[:, : heads * dh]
+    assert np.isfinite(got).all()
+
+    def expect(qkv_in, g_in):
+        x = oracle.ts_variate_attention(qkv_in, kv, group, role, cov, rows, enc, n, heads, dh, d)
+        return (oracle.ts_gate(x, g_in) if g_in is not None else x)[:, : heads * dh]
+
+    exp_r = expect(q.float().cpu().numpy(), gt.float().cpu().numpy() if gt is not None else None)
+    exp = expect(qkv, g)
+    err_r, err = oracle.rel_max_error(got, exp_r), oracle.rel_max_error(got, exp)
+    print(f"  rel err {err_r:.3e} on the rounded inputs, {err:.3e} against fp32", flush=True)
+    assert err_r <= (2.0 ** -8 if dt == "bf16" else 2.0 ** -11)
+    assert err <= 2e-2
 
 
 def test_univariate_rows_output_their_own_v(gpu):
