@@ -33,19 +33,38 @@ def traffic_source(name: str) -> str:
     """Where a roofline's traffic figure comes from: it is read from a committed profile, not measured
     in this run."""
     return (f"profiles/{name}.traffic.json: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE of the same kernel in "
-            f"an earlier run, scaled by a plain copy's counters (not measured in this run)")
+            f"an earlier run, scaled by known-size copy, reduction and fill kernels (not measured in this run)")
+
+
+def _profile(name: str) -> dict:
+    p = ROOT / "profiles" / f"{name}.traffic.json"
+    if not p.exists():
+        return {}
+    try:
+        return json.loads(p.read_text())
+    except Exception:
+        return {}
 
 
 def traffic_from_profile(name: str):
-    """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, scaled by a
-    known-size copy), committed as profiles/<name>.traffic.json; None when not measured."""
-    p = ROOT / "profiles" / f"{name}.traffic.json"
-    if not p.exists():
-        return None
-    try:
-        return json.loads(p.read_text()).get("bytes_per_launch")
-    except Exception:
-        return None
+    """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, scaled by
+    known-size calibration kernels), committed as profiles/<name>.traffic.json; None when not
+    measured."""
+    return _profile(name).get("bytes_per_launch")
+
+
+def from_profile(name: str, frac: float, launch_ms: float) -> dict:
+    """The roofline fields read from a committed profile: the traffic, where it comes from, and the
+    profiled box's own timing of the same kernel (20 launches after 5 warm-ups, as here) with the
+    frac that timing gives and that box's clock from GRBM_GUI_ACTIVE. Boxes of the pool differ by
+    several percent, so this frac and the live one bracket the box-to-box range."""
+    d = _profile(name)
+    out = {"traffic": d.get("bytes_per_launch"), "traffic_source": traffic_source(name)}
+    ms = d.get("launch_ms")
+    if ms:
+        out["profiled_box"] = {"launch_ms": round(ms, 5), "frac": round(frac * launch_ms / ms, 4),
+                               "clock_ghz": d.get("clock_ghz")}
+    return out
 
 
 def cpu_info(threads: int) -> dict:
@@ -143,12 +162,12 @@ def group_attention_line(steps: int, warmup: int, cpu: bool = True) -> dict:
     log(f"group attention: {ms:.4f} ms, {gbs:.0f} GB/s algorithmic ({100 * gbs / PEAK_HBM_GBS:.1f}% of HBM)")
     res = {
         "workload": "config 2: fp32 Chronos-2 group attention, 4096 rows x 129 slots, 12x64, groups U{1..64}",
-        "kernel": "jc::group_attention_f32<64, false, true, false>",
+        "kernel": "jc::group_attention_f32<float, 64, false, true, false>",
         "launch_ms": round(ms, 5),
         "value": round(gbs, 1),
         "unit": "GB/s",
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": traffic_from_profile("c2_group_attention_f32_config2"), "traffic_source": traffic_source("c2_group_attention_f32_config2")},
+                     "frac": round(gbs / PEAK_HBM_GBS, 4), **from_profile("c2_group_attention_f32_config2", gbs / PEAK_HBM_GBS, ms)},
         "bytes_per_launch": nbytes,
         "tflops": round(case.flops() / (ms * 1e-3) / 1e12, 2),
     }
@@ -206,7 +225,7 @@ def time_attention_lowp_line(case, steps: int, warmup: int, dtype_name: str) -> 
         "unit": "TFLOP/s",
         "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tf / PEAK_BF16_TFLOPS, 4),
-                     "traffic": traffic_from_profile(f"c2_time_attention_{dtype_name}_config1"), "traffic_source": traffic_source(f"c2_time_attention_{dtype_name}_config1")},
+                     **from_profile(f"c2_time_attention_{dtype_name}_config1", tf / PEAK_BF16_TFLOPS, ms)},
         "dense_tflops": round(case.dense_flops() / (ms * 1e-3) / 1e12, 2),
     }
     del q16, out
@@ -272,7 +291,7 @@ def layer_line(steps: int, warmup: int, dtype_name: str = "f32") -> dict:
         "tokens_per_s": round(tokens / (ms * 1e-3), 1),
         "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": peak, "unit": "TFLOP/s",
                      "frac": round(tf / peak, 4),
-                     "traffic": traffic_from_profile(f"c2_layer_{dtype_name}_config4"), "traffic_source": traffic_source(f"c2_layer_{dtype_name}_config4")},
+                     **from_profile(f"c2_layer_{dtype_name}_config4", tf / peak, ms)},
         "flops_per_step": flops,
         "gemm_share_of_flops": round(case.gemm_flops() / flops, 4),
     }
@@ -313,7 +332,7 @@ def ts_time_attention_line(steps: int, warmup: int, cpu: bool = True) -> dict:
         "unit": "TFLOP/s",
         "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tf / PEAK_BF16_TFLOPS, 4),
-                     "traffic": traffic_from_profile("ts_time_attention_bf16_config3"), "traffic_source": traffic_source("ts_time_attention_bf16_config3")},
+                     **from_profile("ts_time_attention_bf16_config3", tf / PEAK_BF16_TFLOPS, ms / layers)},
         "dense_tflops": round(layers * 4.0 * case.dh * case.n * case.n * case.heads * case.rows / (ms * 1e-3) / 1e12, 2),
     }
     res["stack"] = ts_stack_timing(case, steps, warmup)
@@ -642,7 +661,7 @@ def ts_block_line(steps: int, warmup: int, dtype_name: str = "f32") -> dict:
         "device_forward_ms": round(dev_ms, 2),
         "device_series_per_s": round(rows / (dev_ms * 1e-3), 1),
         "gemm_tflops": round(gemm_flops / (dev_ms * 1e-3) / 1e12, 2),
-        "traffic_per_call": traffic_from_profile(f"ts_block_{dtype_name}_config3"), "traffic_source": traffic_source(f"ts_block_{dtype_name}_config3"),
+        "traffic_per_device_forward": traffic_from_profile(f"ts_block_{dtype_name}_config3"), "traffic_source": traffic_source(f"ts_block_{dtype_name}_config3"),
     }
     del model
     torch.cuda.empty_cache()
@@ -831,7 +850,7 @@ def main() -> int:
             "peak": PEAK_FP32_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_FP32_TFLOPS, 4),
-            "traffic": traffic_from_profile("c2_time_attention_f32_config1"), "traffic_source": traffic_source("c2_time_attention_f32_config1"),
+            **from_profile("c2_time_attention_f32_config1", achieved / PEAK_FP32_TFLOPS, launch_ms),
             "kernel": "jc::time_attention_f32<64, 32, true, false, true, true, false>",
             "launch_ms": round(launch_ms, 5),
         },
