@@ -20,7 +20,7 @@ OUT_DIR = HERE / "_build"
 LIB = HERE / "libjitcast_hip.so"
 ARCH = os.environ.get("JITCAST_HIP_ARCH", "gfx950")
 
-SOURCES = ["jc_abi.cpp", "jc_blas.cpp", "jc_host.cpp", "ts_host.cpp", "time_attention_f32.hip", "time_attention_lp.hip", "time_attention_lpw.hip", "time_attention_lpp.hip", "gate.hip", "group_attention_f32.hip", "stage_f32.hip", "stage_lp.hip", "c2_tokens.hip", "c2_prep.hip", "ts_block.hip", "ts_ends.hip", "rng.hip"]
+SOURCES = ["jc_abi.cpp", "jc_blas.cpp", "jc_host.cpp", "ts_host.cpp", "time_attention_f32.hip", "time_attention_lp.hip", "time_attention_lpw.hip", "time_attention_lpp.hip", "time_attention_lps.hip", "gate.hip", "group_attention_f32.hip", "stage_f32.hip", "stage_lp.hip", "c2_tokens.hip", "c2_prep.hip", "ts_block.hip", "ts_ends.hip", "rng.hip"]
 
 COMMON = [
     "-O3",

@@ -128,8 +128,9 @@ void prof_clear(jc_ctx* ctx) {
 
 // JITCAST_HIP_LP_KERNEL picks the bf16/fp16 time-attention kernel: "stream" (time_attention_lp,
 // which takes every shape), "wide" (time_attention_lpw) or "persist" (time_attention_lpp), the
-// last two for the shapes they take. Unset, Chronos-2 uses the persistent kernel where it fits,
-// else the row-wide one, and Timestral the streaming one: its row-wide variant holds every token's
+// last two for the shapes they take ("persist" covers time_attention_lpp, rows of 257..513 tokens,
+// and time_attention_lps, rows of 65..160). Unset, Chronos-2 uses a persistent kernel where one
+// fits, else the row-wide one, and Timestral the streaming one: its row-wide variant holds every token's
 // table row in LDS and fits one workgroup per CU (measured on config 3: 6.30 ms against 6.04 ms
 // per 12 layers). Read at every launch, so a host can switch at run time.
 enum LpKernel { kLpStream, kLpWide, kLpPersist };
@@ -471,6 +472,9 @@ static int launch_time(jc_ctx* ctx, const char* W, const jc::TimeArgs& a, int dh
     } else if (lp_choice(ts) == kLpPersist && jc::time_attention_lpp_fits(a, dh, ts)) {
         ProfScope ps(ctx, ts ? "ts time_attention_lpp" : "c2 time_attention_lpp");
         e = jc::time_attention_lpp_launch(a, fp16, ctx->cus, ctx->stream);
+    } else if (lp_choice(ts) == kLpPersist && jc::time_attention_lps_fits(a, dh, ts)) {
+        ProfScope ps(ctx, ts ? "ts time_attention_lps" : "c2 time_attention_lps");
+        e = jc::time_attention_lps_launch(a, fp16, ctx->cus, ctx->stream);
     } else if (lp_choice(ts) != kLpStream && jc::time_attention_lpw_fits(a, dh)) {
         ProfScope ps(ctx, ts ? "ts time_attention_lpw" : "c2 time_attention_lpw");
         e = jc::time_attention_lpw_launch(a, dh, ts, fp16, ctx->stream);

@@ -25,6 +25,8 @@ hipError_t time_attention_lpw_launch(const TimeArgs& a, int dh, bool ts, bool fp
 // 8-wave workgroup per CU streams its (row, head) items; `cus` sizes the grid.
 bool time_attention_lpp_fits(const TimeArgs& a, int dh, bool ts);
 hipError_t time_attention_lpp_launch(const TimeArgs& a, bool fp16, int cus, hipStream_t stream);
+bool time_attention_lps_fits(const TimeArgs& a, int dh, bool ts);
+hipError_t time_attention_lps_launch(const TimeArgs& a, bool fp16, int cus, hipStream_t stream);
 // att[i] *= sigmoid(g[i]) for i < count (dtype: 0 fp32, 1 bf16, 2 fp16)
 hipError_t gate_launch(void* att, const void* g, uint64_t count, int dtype, hipStream_t stream);
 // The arguments of the group-attention kernels (by value).

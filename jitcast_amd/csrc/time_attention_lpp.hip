@@ -32,6 +32,7 @@
 #include "jc_common.hpp"
 #include "jc_kernels.hpp"
 #include "lp_common.hpp"
+#include "lp_stream.hpp"
 #include "time_mask.hpp"
 
 namespace jc {
@@ -53,9 +54,6 @@ constexpr int kMaxBlk = 9;               // 64-key blocks per row at most (n <= 
 constexpr int kPT = kDH + 4;             // floats per RoPE table row in LDS
 constexpr int kMaxN = kPart + 1;         // rows up to 512 tokens plus the [REG] token
 
-typedef float floatx4_t __attribute__((ext_vector_type(4)));
-typedef short shortx4 __attribute__((ext_vector_type(4)));
-
 struct PLds {
     uint16_t kv[kSlots][2][kKB * kDH];  // [slot][K | V][key * 64 + swizzled dim]
     uint16_t q[kW][kTiles][kQ * kDH];   // prefetched raw Q of the next item, per wave and tile
@@ -65,104 +63,6 @@ struct PLds {
     uint64_t mask[kIpw][kMaxBlk];       // live bits per item and block
     uint32_t need[kIpw];                // blocks of an item with a live key
     float reg_part[2][kW][kDH + 2];     // query 512: each wave's share of the output, its max and sum
-};
-
-// element index of (key, 16-byte chunk c) in a swizzled 128-byte-row block
-__device__ __forceinline__ int swz(int key, int c) { return key * kDH + ((c ^ (key & 7)) << 3); }
-
-// The stream's loads, waits and barriers are inline assembly, so the compiler neither sees the
-// direct-to-LDS loads (it would otherwise wait for all of them before any LDS read it cannot prove
-// disjoint) nor moves LDS accesses across a wait or a barrier ("memory" clobbers).
-// 16 bytes per lane from gptr to lds_base + 16 * lane (M0 holds the wave-uniform LDS address).
-__device__ __forceinline__ void dma16(const void* gptr, const void* lds_base) {
-    const uint32_t off = (uint32_t)(size_t)(__attribute__((address_space(3))) const void*)lds_base;
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(off) : "memory", "m0");
-}
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-    static_assert(N >= 0 && N < 64, "vmcnt");
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-// waits until at most n loads are outstanding, rounded down to 0, 2 or 8 (a wait for fewer is
-// always safe: it only waits longer)
-__device__ __forceinline__ void wait_vm_rt(int n) {
-    if (n >= 8) {
-        wait_vm<8>();
-    } else if (n >= 2) {
-        wait_vm<2>();
-    } else {
-        wait_vm<0>();
-    }
-}
-// this wave's LDS writes done, then the workgroup barrier
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-// a copy of x the compiler cannot see through: values derived from it inside a rarely taken path
-// are computed there instead of being hoisted out of the stream loop into long-lived registers
-__device__ __forceinline__ int opaque(int x) {
-    asm volatile("" : "+v"(x));
-    return x;
-}
-
-template <int CTRL>
-__device__ __forceinline__ float dpp(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
-}
-// over the 64 lanes of the wave, result in every lane: quad exchanges and row rotations (DPP),
-// then the row pairs and the wave halves (v_permlane16_swap, v_permlane32_swap)
-__device__ __forceinline__ float wave_max(float v) {
-    v = fmaxf(v, dpp<0xB1>(v));   // quad_perm [1,0,3,2]
-    v = fmaxf(v, dpp<0x4E>(v));   // quad_perm [2,3,0,1]
-    v = fmaxf(v, dpp<0x124>(v));  // row_ror:4
-    v = fmaxf(v, dpp<0x128>(v));  // row_ror:8
-    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return pair_max(fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1])));
-}
-__device__ __forceinline__ float wave_sum(float v) {
-    v += dpp<0xB1>(v);
-    v += dpp<0x4E>(v);
-    v += dpp<0x124>(v);
-    v += dpp<0x128>(v);
-    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return pair_sum(__uint_as_float(r[0]) + __uint_as_float(r[1]));
-}
-
-template <typename T>
-__device__ __forceinline__ floatx4 widen4(u32x2 raw) {
-    typedef T t4 __attribute__((ext_vector_type(4)));
-    t4 v = __builtin_bit_cast(t4, raw);
-    floatx4 r;
-#pragma unroll
-    for (int u = 0; u < 4; u++) r[u] = (float)v[u];
-    return r;
-}
-
-template <typename T>
-struct Mfma16;
-template <>
-struct Mfma16<__bf16> {
-    static __device__ __forceinline__ floatx4 run(bf16x8 a, bf16x8 b, floatx4 c) {
-        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-    }
-};
-template <>
-struct Mfma16<_Float16> {
-    static __device__ __forceinline__ floatx4 run(halfx8 a, halfx8 b, floatx4 c) {
-        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-    }
-};
-
-__device__ __forceinline__ u32x2 read_tr(const uint16_t* p) {
-    auto v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (__attribute__((address_space(3))) shortx4*)((__attribute__((address_space(3))) void*)p));
-    return __builtin_bit_cast(u32x2, v);
-}
-
-// per query tile: output accumulators and the online-softmax state of time_attention_lp.hip
-struct Tile {
-    floatx16 o[2];
-    float m_tot, m_mfma, resid, l_run;
-    bool has_ref, any_resid;
-    uint32_t qx0;
 };
 
 template <typename T, bool ROPE>

@@ -45,8 +45,8 @@ def gpu():
 def lp_kernel(request, monkeypatch):
     """Which bf16/fp16 time-attention kernel the library launches (JITCAST_HIP_LP_KERNEL): the
     streaming one, the row-wide one (rows of 256+ tokens and head width 32 or 64) or the persistent
-    one (Chronos-2 rows of 257..513 tokens, head width 64); a shape the chosen kernel does not take
-    falls back to the row-wide or streaming kernel. Unset, Chronos-2 uses the persistent kernel
+    ones (Chronos-2, head width 64: rows of 257..513 tokens, and the short-row kernel for rows of
+    65..160); a shape the chosen kernel does not take falls back to the row-wide or streaming kernel. Unset, Chronos-2 uses the persistent kernel
     where it fits, Timestral the streaming one."""
     monkeypatch.setenv("JITCAST_HIP_LP_KERNEL", request.param)
     return request.param

@@ -73,8 +73,13 @@ LP_CASES = [c for c in CASES if c[3] % 16 == 0 and c[4] % 8 == 0] + [
     (3, 300, 2, 64, 136, "random"),
     (1, 257, 1, 64, 64, "pad"),
     (2, 512, 3, 64, 192, "random"),
-    (3, 133, 2, 64, 128, "pad"),  # 5 query tiles: one 5-wave workgroup per (row, head)
+    (3, 133, 2, 64, 128, "pad"),  # 5 query tiles: 5 waves per item in the short-row persistent kernel
     (2, 160, 2, 64, 128, "random"),
+    (2, 65, 2, 64, 128, "random"),  # the shortest row the short-row kernel takes: 2 blocks, 3 tiles
+    (3, 96, 2, 64, 128, "pad"),
+    (2, 100, 3, 64, 192, "all"),  # 4 tiles
+    (2, 128, 2, 64, 136, "random"),
+    (1, 64, 2, 64, 128, "random"),  # one block: the streaming kernel
 ]
 
 
@@ -316,17 +321,20 @@ def test_rejects_bad_shapes(gpu):
 
 @pytest.mark.parametrize("dt", sorted(LP_DTYPES))
 @pytest.mark.parametrize("table", [True, False])
-def test_lowp_many_items_per_workgroup(gpu, oracle, dt, table, monkeypatch):
-    """The persistent kernel walks up to 12 (row, head) items per workgroup and streams their blocks
-    back to back: 300 rows x 12 heads at n = 513 gives every workgroup 12 items of different lengths,
-    including a row without live keys (zeros), a row whose only live key is [REG], rows with gaps
-    and left-padded rows. Without a table the kernel takes q and k as already rotated."""
+@pytest.mark.parametrize("n", [513, 133])
+def test_lowp_many_items_per_workgroup(gpu, oracle, dt, table, n, monkeypatch):
+    """The persistent kernels walk several (row, head) items per workgroup and stream their blocks
+    back to back. 300 rows x 12 heads: at n = 513 every workgroup gets 12 items of different lengths;
+    at n = 133 (the short-row kernel) 14 or 15 items split over the workgroup's two halves, so one
+    half idles through the last item's steps where the count is odd. Among the rows: one without
+    live keys (zeros), one whose only live key is the last token, rows with gaps and left-padded
+    rows. Without a table the kernel takes q and k as already rotated."""
     monkeypatch.setenv("JITCAST_HIP_LP_KERNEL", "persist")
-    rows, n, heads, dh = 300, 513, 12, 64
+    rows, heads, dh = 300, 12, 64
     inner = heads * dh
     print(f"case {dt} persist many items table={table} rows={rows} n={n}", flush=True)
     qkv = cases.qkv(61, rows * n, inner, std=0.554)
-    live = cases.left_pad_live(61, rows, n, 256)
+    live = cases.left_pad_live(61, rows, n, 256 if n > 256 else n // 2)
     gaps = cases.random_live(61, rows, n, 0.7)
     live[::3] = gaps[::3]
     live[:, n - 1] = 1
