@@ -82,10 +82,11 @@ __device__ __forceinline__ float quad_sum(float v) {
     return pair_sum(v);
 }
 
-// A position in the wave's job stream: group [gs, ge), query chunk qc (up to kQT tiles of 16
-// rows), head h, key tile kt.
+// A position in the wave's job stream: rows [gs, ge) (one group, or a pack of consecutive groups
+// spanning at most 16 rows), query chunk qc (up to kQT tiles of 16 rows), head h, key tile kt.
 struct Job {
     int gs, ge, qc, h, kt;
+    uint32_t pb;    // group starts of the job relative to gs (bit i = row gs + i); 1 for one group
     uint32_t rest;  // starts of the tile's remaining groups (bit b = row r0 + b)
     bool valid;
 };
@@ -186,7 +187,19 @@ __global__ __launch_bounds__(kWave) void group_attention_f32(const GroupArgs a, 
         jb.qc = 0;
         jb.h = h_lo;
         jb.kt = 0;
+        jb.pb = 1u;
         jb.rest = jb.valid ? rest & (rest - 1) : 0;
+        // small groups starting in the tile share one job while they span at most 16 rows: one
+        // 16 x 16 score tile, masked block-diagonally, instead of one mostly empty tile per group
+        while (jb.rest != 0) {
+            const int b2 = __builtin_ctz(jb.rest);
+            if (r0 + b2 != jb.ge) break;
+            const int e2 = min(max(__builtin_amdgcn_readlane(ge_l, b2), jb.ge + 1), rows);
+            if (e2 - jb.gs > kRT) break;
+            jb.pb |= 1u << (jb.ge - jb.gs);
+            jb.ge = e2;
+            jb.rest &= jb.rest - 1;
+        }
         return jb;
     };
     // key tiles innermost, so a K/V tile is used by every resident query tile right after it lands
@@ -238,10 +251,20 @@ __global__ __launch_bounds__(kWave) void group_attention_f32(const GroupArgs a, 
     floatx4 o_acc[kQT][kM];
     float m_run[kQT], l_run[kQT];
     int q_role[kQT];
+    uint32_t gmask = ~0u;  // a pack's keys in the group of the lane's query row (bit i = row gs + i)
     while (cur.valid) {
         const int tiles = (cur.ge - cur.gs + kRT - 1) / kRT;
         const int nq = min(kQT, tiles - kQT * cur.qc);  // query tiles in this chunk
         if (cur.kt == 0) {
+            // a pack spans one tile: the lane's query row gs + j reads the rows of its own group
+            if (cur.pb != 1u) {
+                const uint32_t upto = (2u << j) - 1u;
+                const int s_q = 31 - __builtin_clz(cur.pb & upto);
+                const uint32_t above = cur.pb & ~upto;
+                gmask = (above ? (1u << __builtin_ctz(above)) - 1u : 0xffffu) & ~((1u << s_q) - 1u);
+            } else {
+                gmask = ~0u;
+            }
             // a new (group, chunk, head): load its query tiles and reset the softmax state
 #pragma unroll
             for (int qi = 0; qi < kQT; qi++) {
@@ -275,7 +298,7 @@ __global__ __launch_bounds__(kWave) void group_attention_f32(const GroupArgs a, 
         for (int qi = 0; qi < kQT; qi++) {
             if (qi < nq) {
                 // the keys query row qrow may read (BlockLayout.variateAllowed for Timestral)
-                uint32_t allowed = vbits;
+                uint32_t allowed = vbits & gmask;
                 if (TS) {
                     const int qrow = cur.gs + kRT * (kQT * cur.qc + qi) + j;
                     uint32_t forbid = 0;
@@ -284,7 +307,7 @@ __global__ __launch_bounds__(kWave) void group_attention_f32(const GroupArgs a, 
                         if (q_role[qi] == 2) forbid |= ~kbits & 0xffffu;  // known rows read known rows only
                     }
                     const int self = qrow - kbase;
-                    allowed = (vbits & ~forbid) | ((self >= 0 && self < kRT) ? (1u << self) : 0u);
+                    allowed = ((vbits & ~forbid) | ((self >= 0 && self < kRT) ? (1u << self) : 0u)) & gmask;
                 }
                 floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll

@@ -15,7 +15,7 @@ Config 4: the Chronos-2 120M-class forecast (d_model 768, 12 x 64, 12 layers, d_
 Two groups run against the oracle's CpuChronos2.forward restatement (fp32 encoder and the f16x3
 encoder, fp16 GEMMs over three-term splits of every fp32 operand: quantiles within 1e-3; the bf16 and
 fp16 encoders' errors are reported and held to 2e-2); the full 1,024-group request is checked for
-finite quantiles and equivariance under permuting the groups.
+finite quantiles and equivariance under permuting the groups (in blocks of 16: whole 16-row tiles).
 """
 import numpy as np
 import pytest
@@ -197,14 +197,18 @@ def test_config4_call_reproducible(gpu, dt):
 
 def test_config4_full_request_properties(gpu):
     """Config 4's full request (1,024 groups, 5,120 rows) through the fp32 encoder: finite quantiles,
-    and permuting the groups permutes the forecasts bit for bit: every kernel computes a row
-    independently of its slot, the GEMMs included (no tile's k range is split over workgroups)."""
+    and permuting the groups in blocks of 16 permutes the forecasts bit for bit. The GEMMs and the
+    time attention compute a row independently of its slot (no GEMM tile's k range is split over
+    workgroups). Group attention packs the small groups that start in a 16-row tile into one job,
+    so a group's sums depend on its place in its tile; 16 groups of 5 are 80 rows, five whole
+    tiles, so moving blocks of them keeps every group's place while every row changes GEMM tiles."""
     print("case config 4 full request fp32: 1024 groups x 5 rows x 2048 steps", flush=True)
     ctx, group, fut, _ = synthetic.c2_forecast_config4()
     model = cm.HipChronos2Model(C4, _c4_weights(), dtype="f32")
     a = model.forecast(ctx, group, fut, h=4)
     assert np.isfinite(a).all()
-    gperm = np.random.default_rng(3).permutation(1024)
+    bperm = np.random.default_rng(3).permutation(1024 // 16)
+    gperm = (bperm[:, None] * 16 + np.arange(16)[None, :]).reshape(-1)
     rows = (gperm[:, None] * 5 + np.arange(5)[None, :]).reshape(-1)
     b = model.forecast(ctx[rows], group[rows], fut[rows], h=4)
     d = float(np.max(np.abs(a[rows].astype(np.float64) - b)) / np.max(np.abs(b)))

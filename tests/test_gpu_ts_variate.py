@@ -42,6 +42,7 @@ CASES = [
     (20, 3, 1, 1, 128, 128, 20, 20, 1, 0.6, True),  # 128-wide heads
     (17, 2, 0, 2, 48, 96, 17, 17, 0, 1.0, False),
     (40, 0, 3, 2, 64, 128, 2, 9, 1, 1.0, False),  # decoder slots only
+    (96, 4, 2, 4, 64, 256, 3, 3, 1, 0.8, True),  # a target and 2 covariates per group: packs of 5 groups
     # one-row groups (univariate series) take the streaming path per 16-row tile
     (80, 7, 2, 12, 64, 768, 1, 1, 1, 0.6, True),
     (21, 3, 1, 2, 128, 256, 1, 1, 0, 0.7, False),
