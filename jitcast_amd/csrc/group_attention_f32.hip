@@ -69,19 +69,6 @@ __device__ __forceinline__ void store4(T* p, floatx4 v) {
     }
 }
 
-// max / sum over the four lanes j, j+16, j+32, j+48 (v_permlane16_swap then v_permlane32_swap)
-__device__ __forceinline__ float quad_max(float v) {
-    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-    return pair_max(v);
-}
-
-__device__ __forceinline__ float quad_sum(float v) {
-    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-    return pair_sum(v);
-}
-
 // A position in the wave's job stream: rows [gs, ge) (one group, or a pack of consecutive groups
 // spanning at most 16 rows), query chunk qc (up to kQT tiles of 16 rows), head h, key tile kt.
 struct Job {

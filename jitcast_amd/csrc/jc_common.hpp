@@ -35,6 +35,19 @@ __device__ __forceinline__ float pair_sum(float v) {
 // 2^x on the hardware transcendental unit (v_exp_f32); exp2(-inf) = 0.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// max / sum over the four lanes j, j+16, j+32, j+48 (v_permlane16_swap then v_permlane32_swap)
+__device__ __forceinline__ float quad_max(float v) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    return pair_max(v);
+}
+
+__device__ __forceinline__ float quad_sum(float v) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    return pair_sum(v);
+}
+
 // The three-term fp16 split of fp32 operands (dtype JC_F16X3): hi = fp16(v) and lo = fp16(v - hi),
 // each saturated to +-65504 as the FP16 GEMM mode's operands are (NaN kept).
 __device__ __forceinline__ _Float16 f16_sat(float v) { return (_Float16)(v != v ? v : fminf(fmaxf(v, -65504.f), 65504.f)); }

@@ -40,6 +40,7 @@
 // X3 (Chronos-2, 64-wide heads; the JC_F16X3 layer): out is the O projection's A operand, fp16
 // rows of 3 * inner values [hi | hi | lo] (the three-term split of each fp32 output value), so the
 // layer needs no separate split pass over the attention output.
+#include "f32_tail.hpp"
 #include "jc_common.hpp"
 #include "jc_kernels.hpp"
 #include "time_mask.hpp"
@@ -166,10 +167,34 @@ __global__ __launch_bounds__(kThreads) void time_attention_f32(const TimeArgs a,
     const int n = a.n, inner = a.inner, half = dh / 2;
     const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
     const int j = lane % 32, g = lane / 32;
-    const uint32_t total = (uint32_t)a.rows * a.heads * a.qgroups;
+    const uint32_t items = (uint32_t)a.rows * a.heads;
+    // With tail workgroups (q_tail > 0), every 4 (row, head) items get their qgroups main
+    // workgroups followed by one tail workgroup whose 4 waves take the items' last R queries; the
+    // neighbouring logical workgroups run on one XCD, so the tail's K/V reads find them in its L2.
+    constexpr bool kTailOk = !TS && !FOLD && EXACT && DHP == 64 && KB == 32;  // FOLD rows have R = 1
+    const bool tails = kTailOk && a.q_tail > 0;
+    const uint32_t per_group = 4 * a.qgroups + 1;
+    const uint32_t total = tails ? (items + 3) / 4 * per_group : items * a.qgroups;
     const uint32_t logical = xcd_remap(blockIdx.x, total);
-    const int qg = logical % a.qgroups;
-    const int bh = logical / a.qgroups;
+    int qg, bh;
+    if (tails) {
+        const uint32_t grp = logical / per_group, s = logical % per_group;
+        if (s == 4 * (uint32_t)a.qgroups) {
+            const uint32_t item = 4 * grp + tid / kWave;
+            if constexpr (kTailOk) {
+                if (item < items)
+                    f32_tail_item<ROPE, X3>(a, item / a.heads, item % a.heads, a.q_tail, tid % kWave);
+            }
+            return;  // the whole workgroup: tail workgroups take no barrier
+        }
+        const uint32_t item = 4 * grp + s / a.qgroups;
+        if (item >= items) return;  // the last group's missing items: before any barrier
+        qg = s % a.qgroups;
+        bh = item;
+    } else {
+        qg = logical % a.qgroups;
+        bh = logical / a.qgroups;
+    }
     const int h = bh % a.heads, r = bh / a.heads;
     const bool fold = FOLD && qg == a.qgroups - 1;  // this workgroup also computes query n - 1
     // key n - 1 alone in the last block: taken on VALU after the loop
@@ -612,6 +637,15 @@ static void launch_f32_rope(const TimeArgs& a, int dh, uint64_t grid, hipStream_
     }
 }
 
+// R when a row of 128k + R tokens, 2 <= R <= 16, takes tail workgroups for its last R queries
+// (Chronos-2, 64-wide heads, no gate), else 0
+static int tail_rows(const TimeArgs& a, int dh) {
+    if (dh != 64 || a.gate || a.q_begin != 0 || a.n <= kWaves * kQ) return 0;
+    if (a.table && a.table_rows < a.n) return 0;
+    const int R = a.n % (kWaves * kQ);
+    return R >= 2 && R <= kTailT ? R : 0;
+}
+
 template <int DHP, bool TS, bool EXACT, bool X3 = false>
 static hipError_t launch_f32(TimeArgs a, int dh, hipStream_t stream) {
     constexpr int KB = 32;  // 32-key blocks (64 measured slower on config 1)
@@ -620,7 +654,17 @@ static hipError_t launch_f32(TimeArgs a, int dh, hipStream_t stream) {
     constexpr bool kCanFold = !TS && EXACT && DHP == 64;
     const bool fold = kCanFold && a.n > 1 && a.n % (kWaves * kQ) == 1;
     a.qgroups = fold ? (a.n - 1) / (kWaves * kQ) : (tiles + kWaves - 1) / kWaves;
-    const uint64_t grid = (uint64_t)a.rows * a.heads * a.qgroups;
+    // rows of 128k + R tokens, 2 <= R <= 16 (Chronos-2, 64-wide heads): the main workgroups take the
+    // first 128k queries and tail workgroups (f32_tail.hpp) the last R, instead of a fifth main
+    // workgroup that stages every block for one partly filled wave
+    int tail = 0;
+    if constexpr (kCanFold) tail = tail_rows(a, dh);
+    if (tail) {
+        a.qgroups = (a.n - tail) / (kWaves * kQ);
+        a.q_tail = a.n - tail;
+    }
+    const uint64_t items = (uint64_t)a.rows * a.heads;
+    const uint64_t grid = tail ? (items + 3) / 4 * (4 * a.qgroups + 1) : items * a.qgroups;
     if constexpr (kCanFold) {
         if (fold) {
             launch_f32_rope<DHP, KB, TS, EXACT, true, X3>(a, dh, grid, stream);

@@ -41,6 +41,8 @@ struct TimeArgs {
     float qscale;           // score scale times log2(e), folded into q
     int qgroups;            // workgroups per (row, head)
     int q_begin;            // the first query the launch covers (0: all of them)
+    int q_tail;             // fp32 Chronos-2 rows of 128k + R: the first query of the tail workgroups
+                            // (0: none), set by the fp32 launcher
 };
 
 template <bool TS>

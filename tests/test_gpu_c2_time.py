@@ -225,15 +225,20 @@ def test_fp32_folded_last_query(gpu, oracle, n, kind):
 
 
 @pytest.mark.parametrize("n,kind,table", [(130, "pad", True), (133, "random", True), (136, "all", True),
-                                          (261, "pad", True), (133, "pad", False), (137, "pad", True)])
+                                          (261, "pad", True), (133, "pad", False), (137, "pad", True),
+                                          (144, "random", True), (145, "pad", True), (130, "random", False),
+                                          (133, "dead", True)])
 def test_fp32_tail_queries(gpu, oracle, n, kind, table):
     """Rows of 128k + R tokens (the forecasts' 128 patches + [REG] + 4 future patches give R = 5):
-    the R tail queries run in a workgroup of their own. Against the oracle, the tail rows checked on
-    their own per head."""
+    with 2 <= R <= 16 the main kernel runs the first 128k queries and a kernel of its own the R tail
+    queries (R = 17 keeps a fifth workgroup). Against the oracle, the tail rows checked on their own
+    per head; "dead": one row without live keys, whose outputs are zeros."""
     rows, heads, dh, inner = 3, 3, 64, 200
     print(f"case tail queries n={n} {kind} table={table}", flush=True)
     qkv = cases.qkv(43, rows * n, inner)
-    live = _live(kind, 43, rows, n)
+    live = _live("pad" if kind == "dead" else kind, 43, rows, n)
+    if kind == "dead":
+        live[1] = 0
     got = _run(qkv, live, rows, n, heads, dh, inner, table=table).reshape(rows, n, inner)
     if table:
         exp = oracle.c2_time_attention(qkv, live, rows, n, heads, dh, inner).reshape(rows, n, inner)
@@ -250,6 +255,8 @@ def test_fp32_tail_queries(gpu, oracle, n, kind, table):
     for h in range(heads):
         sl = np.s_[:, n - tail:, h * dh:(h + 1) * dh]
         assert oracle.rel_max_error(got[sl], exp[sl]) <= TOL_F32, h
+    if kind == "dead":
+        assert not np.any(got[1, :, : heads * dh])
     assert np.isnan(got[:, :, heads * dh:]).all(), "columns past heads * dh are not written"
 
 
