@@ -24,6 +24,8 @@
 //                         (16c+8a+4g+u -> 16c+8g+4a+u) so the same 8 keys are one 16-byte read.
 // Queries along lanes put one query's softmax state in lanes j and j+32: the block max is one
 // v_permlane32_swap.
+#include <type_traits>
+
 #include "jc_common.hpp"
 #include "jc_kernels.hpp"
 #include "lp_common.hpp"
@@ -159,8 +161,13 @@ struct LpStage {
     }
 };
 
+// 3 waves per SIMD where the kernel fits 168 VGPRs without spilling (Timestral's fp16 instance
+// would spill 12 bytes per lane)
+template <typename T, bool TS>
+constexpr bool kLp3Waves = !TS || std::is_same_v<T, __bf16>;
+
 template <typename T, int DHP, int NW, bool ROPE, bool TS, bool EXACT>
-__global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(NW >= 4 && DHP <= 64 && !TS ? 3 : 2)))
+__global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(NW >= 4 && DHP <= 64 && kLp3Waves<T, TS> ? 3 : 2)))
 void time_attention_lp(const TimeArgs a, int dh_rt) {
     const int dh = EXACT ? DHP : dh_rt;
     static_assert(DHP % 16 == 0 && DHP <= 128, "head width");
@@ -358,13 +365,16 @@ void time_attention_lp(const TimeArgs a, int dh_rt) {
             }
             // reg rho of tile sb in lane (j, g) holds key 32sb + 8*(rho/4) + 4g + rho%4 of the block
             if (!uniform) {
+                // one 32-bit word per sub-tile, shifted to the lane's keys: the 64-bit word tested
+                // per score held so many registers that Timestral's instance ran 2 waves per SIMD
 #pragma unroll
-                for (int sb = 0; sb < kSub; sb++)
+                for (int sb = 0; sb < kSub; sb++) {
+                    // bits 8k + u of w: key 32sb + 8k + 4g + u, i.e. reg rho = 4k + u
+                    const uint32_t w = (uint32_t)(allowed >> (32 * sb)) >> (4 * g);
 #pragma unroll
-                    for (int rho = 0; rho < 16; rho++) {
-                        const int bit = 32 * sb + 8 * (rho / 4) + 4 * g + (rho % 4);
-                        if (!((allowed >> bit) & 1ull)) s_acc[sb][rho] = -INFINITY;
-                    }
+                    for (int rho = 0; rho < 16; rho++)
+                        if (!((w >> (8 * (rho / 4) + rho % 4)) & 1u)) s_acc[sb][rho] = -INFINITY;
+                }
             }
             x8 p[kSub][2];
             auto exps = [&](float shift) {
