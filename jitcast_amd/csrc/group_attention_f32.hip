@@ -45,6 +45,40 @@ namespace jc {
 namespace {
 
 constexpr int kRT = 16;  // rows per tile (queries and keys)
+constexpr float kF16Max = 65504.f;
+
+// The fp32 path's products on fp16 MFMA: v = hi + lo with hi = fp16(v) and lo = fp16(v - hi), both
+// rounded to nearest, for |v| <= 65504: hi + lo is within 2^-22 |v| + 2^-25 of v (lo's rounding;
+// where lo is subnormal its step 2^-24 sets the absolute term). A product a.b becomes
+// a_hi.b_hi + a_hi.b_lo + a_lo.b_hi, accumulated in fp32: fp16 products are exact in fp32, so each
+// is within about 2^-20 |a.b| + 2^-25 (|a| + |b|) of a.b.
+// v - h for the low (HI = false) or high half h of a packed fp16 pair, exact in fp32 (one
+// v_fma_mix_f32: v * 1 - h, rounded once)
+template <bool HI>
+__device__ __forceinline__ float sub_half(float v, uint32_t h) {
+    float r;
+    if constexpr (HI) {
+        asm("v_fma_mix_f32 %0, %1, 1.0, -%2 op_sel:[0,0,1] op_sel_hi:[0,0,1]" : "=v"(r) : "v"(v), "v"(h));
+    } else {
+        asm("v_fma_mix_f32 %0, %1, 1.0, -%2 op_sel_hi:[0,0,1]" : "=v"(r) : "v"(v), "v"(h));
+    }
+    return r;
+}
+__device__ __forceinline__ void split_f16(floatx4 v, halfx4& hi, halfx4& lo) {
+    hi = __builtin_convertvector(v, halfx4);
+    const lp::u32x2 h = __builtin_bit_cast(lp::u32x2, hi);
+    const floatx4 r{sub_half<false>(v[0], h[0]), sub_half<true>(v[1], h[0]), sub_half<false>(v[2], h[1]),
+                    sub_half<true>(v[3], h[1])};
+    lo = __builtin_convertvector(r, halfx4);
+}
+__device__ __forceinline__ floatx4 v4(const float (&v)[4]) { return floatx4{v[0], v[1], v[2], v[3]}; }
+// max(acc, |a|, |b|) in one v_max3_f32 (a NaN operand is ignored, as by fmaxf)
+__device__ __forceinline__ float abs_max3(float acc, float a, float b) {
+    float r;
+    asm("v_max3_f32 %0, |%1|, |%2|, %3" : "=v"(r) : "v"(a), "v"(b), "v"(acc));
+    return r;
+}
+__device__ __forceinline__ float abs_max4(float acc, floatx4 v) { return abs_max3(abs_max3(acc, v[0], v[1]), v[2], v[3]); }
 
 // four consecutive storage values as fp32 (one 16- or 8-byte load), and back
 template <typename T>
@@ -230,60 +264,79 @@ __global__ __launch_bounds__(kWave) void group_attention_f32(const GroupArgs a, 
         }
     };
 
-    Job cur = first_of(starts);
-    Kv dc, dn;
-    load_kv(cur, dc);
+    // The job stream. SPLIT (fp32 storage): QK^T and PV as three fp16 MFMA products each
+    // (split_f16), a quarter of the fp32 MFMA cycles. It gives up, returning false, at the first
+    // query, key or value outside fp16's range (or infinite); the wave then runs its whole stream
+    // again on fp32 MFMA, which writes every output of the wave anew.
+    auto stream = [&](auto split_tag) -> bool {
+        constexpr bool SPLIT = decltype(split_tag)::value;
+        Job cur = first_of(starts);
+        Kv dc, dn;
+        load_kv(cur, dc);
 
-    float qreg[kQT][4 * kM];  // resident query tiles (B operand), scaled by qscale
-    floatx4 o_acc[kQT][kM];
-    float m_run[kQT], l_run[kQT];
-    int q_role[kQT];
-    uint32_t gmask = ~0u;  // a pack's keys in the group of the lane's query row (bit i = row gs + i)
-    while (cur.valid) {
-        const int tiles = (cur.ge - cur.gs + kRT - 1) / kRT;
-        const int nq = min(kQT, tiles - kQT * cur.qc);  // query tiles in this chunk
-        if (cur.kt == 0) {
-            // a pack spans one tile: the lane's query row gs + j reads the rows of its own group
-            if (cur.pb != 1u) {
-                const uint32_t upto = (2u << j) - 1u;
-                const int s_q = 31 - __builtin_clz(cur.pb & upto);
-                const uint32_t above = cur.pb & ~upto;
-                gmask = (above ? (1u << __builtin_ctz(above)) - 1u : 0xffffu) & ~((1u << s_q) - 1u);
-            } else {
-                gmask = ~0u;
-            }
-            // a new (group, chunk, head): load its query tiles and reset the softmax state
-#pragma unroll
-            for (int qi = 0; qi < kQT; qi++) {
-                if (qi < nq) {
-                    const int qrow = min(cur.gs + kRT * (kQT * cur.qc + qi) + j, cur.ge - 1);
-                    const T* qp = qkv + ((size_t)qrow * tok_n + t) * stride + cur.h * dh + 4 * g;
-#pragma unroll
-                    for (int m = 0; m < kM; m++) {
-                        floatx4 x = (EXACT || 16 * m + 4 * g < dh) ? load4(qp + 16 * m) : floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                        for (int u = 0; u < 4; u++) qreg[qi][4 * m + u] = x[u] * a.qscale;
-                    }
-                    q_role[qi] = cov ? a.role[qrow] : 0;
+        // resident query tiles (B operand), scaled by qscale: fp32, or (SPLIT) their fp16 pairs
+        float qreg[SPLIT ? 1 : kQT][4 * kM];
+        halfx4 qhi[SPLIT ? kQT : 1][kM], qlo[SPLIT ? kQT : 1][kM];
+        floatx4 o_acc[kQT][kM];
+        float m_run[kQT], l_run[kQT];
+        int q_role[kQT];
+        uint32_t gmask = ~0u;  // a pack's keys in the group of the lane's query row (bit i = row gs + i)
+        while (cur.valid) {
+            const int tiles = (cur.ge - cur.gs + kRT - 1) / kRT;
+            const int nq = min(kQT, tiles - kQT * cur.qc);  // query tiles in this chunk
+            if (cur.kt == 0) {
+                // a pack spans one tile: the lane's query row gs + j reads the rows of its own group
+                if (cur.pb != 1u) {
+                    const uint32_t upto = (2u << j) - 1u;
+                    const int s_q = 31 - __builtin_clz(cur.pb & upto);
+                    const uint32_t above = cur.pb & ~upto;
+                    gmask = (above ? (1u << __builtin_ctz(above)) - 1u : 0xffffu) & ~((1u << s_q) - 1u);
+                } else {
+                    gmask = ~0u;
                 }
+                // a new (group, chunk, head): load its query tiles and reset the softmax state
+                float q_abs = 0.f;
 #pragma unroll
-                for (int m = 0; m < kM; m++) o_acc[qi][m] = floatx4{0.f, 0.f, 0.f, 0.f};
-                m_run[qi] = -INFINITY;
-                l_run[qi] = 0.f;
+                for (int qi = 0; qi < kQT; qi++) {
+                    if (qi < nq) {
+                        const int qrow = min(cur.gs + kRT * (kQT * cur.qc + qi) + j, cur.ge - 1);
+                        const T* qp = qkv + ((size_t)qrow * tok_n + t) * stride + cur.h * dh + 4 * g;
+#pragma unroll
+                        for (int m = 0; m < kM; m++) {
+                            const floatx4 x = ((EXACT || 16 * m + 4 * g < dh) ? load4(qp + 16 * m)
+                                                                             : floatx4{0.f, 0.f, 0.f, 0.f}) *
+                                              a.qscale;
+                            if constexpr (SPLIT) {
+                                q_abs = abs_max4(q_abs, x);
+                                split_f16(x, qhi[qi][m], qlo[qi][m]);
+                            } else {
+#pragma unroll
+                                for (int u = 0; u < 4; u++) qreg[qi][4 * m + u] = x[u];
+                            }
+                        }
+                        if (cov) q_role[qi] = a.role[qrow];
+                    }
+#pragma unroll
+                    for (int m = 0; m < kM; m++) o_acc[qi][m] = floatx4{0.f, 0.f, 0.f, 0.f};
+                    m_run[qi] = -INFINITY;
+                    l_run[qi] = 0.f;
+                }
+                if constexpr (SPLIT) {
+                    if (__ballot(!(q_abs <= kF16Max)) != 0) return false;
+                }
             }
-        }
-        const Job nxt = advance(cur);
-        load_kv(nxt, dn);  // in flight under this job's MFMAs (an invalid job reloads in-bounds rows)
-        __builtin_amdgcn_sched_barrier(0);
+            const Job nxt = advance(cur);
+            load_kv(nxt, dn);  // in flight under this job's MFMAs (an invalid job reloads in-bounds rows)
+            __builtin_amdgcn_sched_barrier(0);
 
-        // bit b: key gs + 16kt + b is valid (and, for Timestral, a target / known-covariate row)
-        const uint32_t vbits = (uint32_t)__ballot(dc.valid != 0) & 0xffffu;
-        const uint32_t tbits = cov ? (uint32_t)__ballot(g == 0 && dc.role == 0) & 0xffffu : 0u;
-        const uint32_t kbits = cov ? (uint32_t)__ballot(g == 0 && dc.role == 2) & 0xffffu : 0u;
-        const int kbase = cur.gs + kRT * cur.kt;
-#pragma unroll
-        for (int qi = 0; qi < kQT; qi++) {
-            if (qi < nq) {
+            // bit b: key gs + 16kt + b is valid (and, for Timestral, a target / known-covariate row)
+            const uint32_t vbits = (uint32_t)__ballot(dc.valid != 0) & 0xffffu;
+            const uint32_t tbits = cov ? (uint32_t)__ballot(g == 0 && dc.role == 0) & 0xffffu : 0u;
+            const uint32_t kbits = cov ? (uint32_t)__ballot(g == 0 && dc.role == 2) & 0xffffu : 0u;
+            const int kbase = cur.gs + kRT * cur.kt;
+            // query tile qi's scores s (reg r of lane (j, g): key 16kt + 4g + r) to the online
+            // softmax's weights, in place; returns the factor that rescales the tile's earlier sums
+            auto softmax = [&](int qi, floatx4& s) {
                 // the keys query row qrow may read (BlockLayout.variateAllowed for Timestral)
                 uint32_t allowed = vbits & gmask;
                 if (TS) {
@@ -296,16 +349,6 @@ __global__ __launch_bounds__(kWave) void group_attention_f32(const GroupArgs a, 
                     const int self = qrow - kbase;
                     allowed = ((vbits & ~forbid) | ((self >= 0 && self < kRT) ? (1u << self) : 0u)) & gmask;
                 }
-                floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int m = 0; m < kM; m++) {
-                    if (EXACT || 16 * m < dh) {
-#pragma unroll
-                        for (int u = 0; u < 4; u++)
-                            s = __builtin_amdgcn_mfma_f32_16x16x4f32(dc.k[m][u], qreg[qi][4 * m + u], s, 0, 0, 0);
-                    }
-                }
-                // reg r of lane (j, g) is key 16kt + 4g + r of the group (every row of the job is in it)
 #pragma unroll
                 for (int r = 0; r < 4; r++) s[r] = ((allowed >> (4 * g + r)) & 1u) ? s[r] : -INFINITY;
                 const float mx = quad_max(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])));
@@ -316,55 +359,114 @@ __global__ __launch_bounds__(kWave) void group_attention_f32(const GroupArgs a, 
 #pragma unroll
                 for (int r = 0; r < 4; r++) s[r] = fast_exp2(s[r] - m_use);
                 l_run[qi] = l_run[qi] * alpha + (s[0] + s[1]) + (s[2] + s[3]);
+                return alpha;
+            };
+            if constexpr (SPLIT) {
+                float kv_abs = 0.f;
+#pragma unroll
+                for (int m = 0; m < kM; m++) kv_abs = abs_max4(abs_max4(kv_abs, dc.k[m]), v4(dc.v[m]));
+                if (__ballot(!(kv_abs <= kF16Max)) != 0) return false;
+                halfx4 khi[kM], klo[kM], vhi[kM], vlo[kM];
 #pragma unroll
                 for (int m = 0; m < kM; m++) {
-                    if (EXACT || 16 * m < dh) {
-                        o_acc[qi][m] *= alpha;
+                    split_f16(dc.k[m], khi[m], klo[m]);
+                    split_f16(v4(dc.v[m]), vhi[m], vlo[m]);
+                }
 #pragma unroll
-                        for (int c = 0; c < 4; c++)
-                            o_acc[qi][m] =
-                                __builtin_amdgcn_mfma_f32_16x16x4f32(dc.v[m][c], s[c], o_acc[qi][m], 0, 0, 0);
+                for (int qi = 0; qi < kQT; qi++) {
+                    if (qi < nq) {
+                        // S^T = K_hi Q_hi + K_hi Q_lo + K_lo Q_hi
+                        floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                        for (int m = 0; m < kM; m++) {
+                            if (EXACT || 16 * m < dh) {
+                                s = __builtin_amdgcn_mfma_f32_16x16x16f16(khi[m], qhi[qi][m], s, 0, 0, 0);
+                                s = __builtin_amdgcn_mfma_f32_16x16x16f16(khi[m], qlo[qi][m], s, 0, 0, 0);
+                                s = __builtin_amdgcn_mfma_f32_16x16x16f16(klo[m], qhi[qi][m], s, 0, 0, 0);
+                            }
+                        }
+                        const float alpha = softmax(qi, s);
+                        // O^T += V_hi P_hi + V_hi P_lo + V_lo P_hi (P in [0, 1])
+                        halfx4 phi, plo;
+                        split_f16(s, phi, plo);
+#pragma unroll
+                        for (int m = 0; m < kM; m++) {
+                            if (EXACT || 16 * m < dh) {
+                                floatx4 acc = o_acc[qi][m] * alpha;
+                                acc = __builtin_amdgcn_mfma_f32_16x16x16f16(vhi[m], phi, acc, 0, 0, 0);
+                                acc = __builtin_amdgcn_mfma_f32_16x16x16f16(vhi[m], plo, acc, 0, 0, 0);
+                                o_acc[qi][m] = __builtin_amdgcn_mfma_f32_16x16x16f16(vlo[m], phi, acc, 0, 0, 0);
+                            }
+                        }
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int qi = 0; qi < kQT; qi++) {
+                    if (qi < nq) {
+                        floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                        for (int m = 0; m < kM; m++) {
+                            if (EXACT || 16 * m < dh) {
+#pragma unroll
+                                for (int u = 0; u < 4; u++)
+                                    s = __builtin_amdgcn_mfma_f32_16x16x4f32(dc.k[m][u], qreg[qi][4 * m + u], s, 0, 0, 0);
+                            }
+                        }
+                        const float alpha = softmax(qi, s);
+#pragma unroll
+                        for (int m = 0; m < kM; m++) {
+                            if (EXACT || 16 * m < dh) {
+                                o_acc[qi][m] *= alpha;
+#pragma unroll
+                                for (int c = 0; c < 4; c++)
+                                    o_acc[qi][m] =
+                                        __builtin_amdgcn_mfma_f32_16x16x4f32(dc.v[m][c], s[c], o_acc[qi][m], 0, 0, 0);
+                            }
+                        }
                     }
                 }
             }
-        }
 
-        if (cur.kt == tiles - 1) {
+            if (cur.kt == tiles - 1) {
 #pragma unroll
-            for (int qi = 0; qi < kQT; qi++) {
-                if (qi < nq) {
-                    const float l = quad_sum(l_run[qi]);
-                    const int qrow = cur.gs + kRT * (kQT * cur.qc + qi) + j;
-                    if (qrow < cur.ge) {
-                        const float inv = l > 0.f ? 1.f / l : 0.f;
-                        const size_t off = ((size_t)qrow * tok_n + t) * inner + cur.h * dh + 4 * g;
-                        // O^T reg r of lane (j, g) in dim tile m is dim 16m + 4g + r of the query
+                for (int qi = 0; qi < kQT; qi++) {
+                    if (qi < nq) {
+                        const float l = quad_sum(l_run[qi]);
+                        const int qrow = cur.gs + kRT * (kQT * cur.qc + qi) + j;
+                        if (qrow < cur.ge) {
+                            const float inv = l > 0.f ? 1.f / l : 0.f;
+                            const size_t off = ((size_t)qrow * tok_n + t) * inner + cur.h * dh + 4 * g;
+                            // O^T reg r of lane (j, g) in dim tile m is dim 16m + 4g + r of the query
 #pragma unroll
-                        for (int m = 0; m < kM; m++) {
-                            if (EXACT || 16 * m + 4 * g < dh) {
-                                floatx4 v = o_acc[qi][m] * inv;
-                                if (gate) {
-                                    // the output gate: att * sigmoid(g) (CpuTimestral.java:156-161)
-                                    const floatx4 gv = load4(gate + off + 16 * m);
+                            for (int m = 0; m < kM; m++) {
+                                if (EXACT || 16 * m + 4 * g < dh) {
+                                    floatx4 v = o_acc[qi][m] * inv;
+                                    if (gate) {
+                                        // the output gate: att * sigmoid(g) (CpuTimestral.java:156-161)
+                                        const floatx4 gv = load4(gate + off + 16 * m);
 #pragma unroll
-                                    for (int u = 0; u < 4; u++) v[u] *= 1.f / (1.f + fast_exp2(-gv[u] * kLog2e));
-                                }
-                                if constexpr (X3) {
-                                    store_split_row(
-                                        static_cast<_Float16*>(a.out) + ((size_t)qrow * tok_n + t) * 3 * inner,
-                                        inner, cur.h * dh + 4 * g + 16 * m, v);
-                                } else {
-                                    store4(out + off + 16 * m, v);
+                                        for (int u = 0; u < 4; u++) v[u] *= 1.f / (1.f + fast_exp2(-gv[u] * kLog2e));
+                                    }
+                                    if constexpr (X3) {
+                                        store_split_row(
+                                            static_cast<_Float16*>(a.out) + ((size_t)qrow * tok_n + t) * 3 * inner,
+                                            inner, cur.h * dh + 4 * g + 16 * m, v);
+                                    } else {
+                                        store4(out + off + 16 * m, v);
+                                    }
                                 }
                             }
                         }
                     }
                 }
             }
+            cur = nxt;
+            dc = dn;
         }
-        cur = nxt;
-        dc = dn;
-    }
+        return true;
+    };
+    if (!stream(std::bool_constant<std::is_same_v<T, float>>{})) stream(std::false_type{});
 }
 
 }  // namespace

@@ -125,3 +125,26 @@ def test_one_row_groups_output_v_or_zeros(gpu):
     got = _run(qkv, live, np.arange(rows, dtype=np.int32), rows, n, heads, dh, inner)
     exp = np.where(live.reshape(-1, 1) != 0, qkv[:, 2 * inner:], np.float32(0))
     np.testing.assert_array_equal(got, exp)
+
+
+@pytest.mark.parametrize("part,scale", [("q", 6e4), ("k", 1e5), ("v", 3e5)])
+def test_fp32_values_beyond_fp16_range(gpu, oracle, part, scale):
+    """fp32 storage runs QK^T and PV as fp16 pairs (hi + lo); a query (after its log2(e) scale), key
+    or value beyond fp16's range (|x| > 65504) sends the wave's whole stream to fp32 MFMA. One row's
+    head-1 piece at one slot is scaled past that range: every output stays within the fp32 bar,
+    those of the groups that never see the row included."""
+    rows, n, heads, dh, inner = 70, 3, 2, 64, 128
+    print(f"case {part} x {scale:g}", flush=True)
+    qkv = cases.qkv(49, rows * n, inner)
+    live = cases.random_live(49, rows, n, 0.9)
+    live[20, 1] = 1
+    group = cases.group_sizes(49, rows, 2, 17)
+    x = qkv.reshape(rows, n, 3, inner)
+    x[20, 1, "qkv".index(part), dh:2 * dh] *= np.float32(scale)
+    assert np.abs(x[20, 1, "qkv".index(part), dh:2 * dh]).max() * (np.log2(np.e) if part == "q" else 1) > 65504
+    got = _run(qkv, live, group, rows, n, heads, dh, inner)
+    exp = oracle.c2_group_attention(qkv, live, group, rows, n, heads, dh, inner)
+    assert np.isfinite(got).all()
+    assert oracle.rel_max_error(got, exp) <= TOL_F32
+    other = np.repeat(group != group[20], n)  # token rows of the groups without row 20
+    assert oracle.rel_max_error(got[other], exp[other]) <= TOL_F32
