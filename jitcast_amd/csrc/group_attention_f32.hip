@@ -131,9 +131,13 @@ __global__ __launch_bounds__(kWave) void group_attention_f32(const GroupArgs a, 
     const int lane = threadIdx.x;
     const int j = lane % 16, g = lane / 16;
     const uint32_t total = (uint32_t)a.rtiles * n * a.hsplit;
-    const uint32_t logical = xcd_remap(blockIdx.x, total);
+    // With a tile order: blocks in that order (tile, then slot, then head range), heaviest first, so
+    // the last waves of the launch are light ones; consecutive blocks go to different XCDs, which
+    // balances them. Without: tiles fastest within each slot, each XCD a contiguous range.
+    const uint32_t logical = a.order ? blockIdx.x : xcd_remap(blockIdx.x, total);
     const uint32_t tile_slot = logical / a.hsplit;
-    const int t = tile_slot / a.rtiles, rt = tile_slot % a.rtiles;
+    const int t = a.order ? (int)(tile_slot % n) : (int)(tile_slot / a.rtiles);
+    const int rt = a.order ? a.order[tile_slot / n] : (int)(tile_slot % a.rtiles);
     // this wave's heads [h_lo, h_hi): a (tile, slot)'s heads are split over hsplit waves, so the
     // tiles where long groups start do not hold one wave for all heads while their neighbours idle
     const int hs = logical % a.hsplit;
@@ -482,10 +486,57 @@ static int group_head_split() {
     return v >= 1 && v <= 16 ? v : 4;
 }
 
+constexpr int kOrderBuckets = 64;
+
+// A counting sort of the tiles by work into buckets, 0 for the most: a group's jobs per head are its
+// key tiles times its query tiles, (ceil(g / 16))^2 for a group of g rows (bounds clamped as the
+// kernel clamps them), summed over the groups starting in the tile. One row per lane (16 lanes a
+// tile, summed by shuffles), the buckets in LDS, one wave's scan of the counts, then the scatter.
+// Ties come out in any order: which block runs a tile changes nothing in its results.
+__global__ __launch_bounds__(1024) void group_tile_order(const int32_t* gstart, const int32_t* gend, int rows,
+                                                         int32_t* order) {
+    __shared__ int slot[kOrderBuckets];
+    __shared__ uint8_t bucket[kGroupOrderTiles];
+    const int tid = threadIdx.x, rtiles = (rows + kRT - 1) / kRT;
+    if (tid < kOrderBuckets) slot[tid] = 0;
+    __syncthreads();
+    for (int r = tid; r < rtiles * kRT; r += blockDim.x) {  // blockDim.x is a multiple of 16
+        int w = 0;
+        if (r < rows) {
+            const int gs = gstart[r], ge = gend[r];
+            if (gs == r) {
+                const int kt = min((min(max(ge, r + 1), rows) - r + kRT - 1) / kRT, kOrderBuckets);
+                w = kt * kt;
+            }
+        }
+#pragma unroll
+        for (int o = kRT / 2; o > 0; o >>= 1) w += __shfl_xor(w, o, kRT);
+        if (r % kRT == 0) {
+            const int b = kOrderBuckets - 1 - min(w, kOrderBuckets - 1);
+            bucket[r / kRT] = (uint8_t)b;
+            atomicAdd(&slot[b], 1);
+        }
+    }
+    __syncthreads();
+    if (tid < kOrderBuckets) {  // wave 0: exclusive prefix sum of the counts
+        const int c = slot[tid];
+        int x = c;
+#pragma unroll
+        for (int o = 1; o < kOrderBuckets; o <<= 1) {
+            const int y = __shfl_up(x, o);
+            if (tid >= o) x += y;
+        }
+        slot[tid] = x - c;
+    }
+    __syncthreads();
+    for (int tile = tid; tile < rtiles; tile += blockDim.x) order[atomicAdd(&slot[bucket[tile]], 1)] = tile;
+}
+
 template <typename T, int DHP, bool TS, bool EXACT, bool X3 = false>
 static hipError_t launch_group(GroupArgs a, int dh, hipStream_t stream) {
     a.rtiles = (a.rows + kRT - 1) / kRT;
     a.hsplit = std::min(group_head_split(), a.heads);
+    if (a.rtiles > kGroupOrderTiles) a.order = nullptr;
     const uint64_t grid = (uint64_t)a.rtiles * a.n * a.hsplit;
     if (grid > 0xffffffffull) return hipErrorInvalidValue;
     hipLaunchKernelGGL((group_attention_f32<T, DHP, TS, EXACT, X3>), dim3((uint32_t)grid), dim3(kWave), 0, stream, a,
@@ -521,6 +572,13 @@ hipError_t group_attention_launch(const GroupArgs& a, int dh, bool ts, int dtype
         case 2: return dispatch_group_type<_Float16>(a, dh, ts, stream);
         default: return hipErrorInvalidValue;
     }
+}
+
+hipError_t group_tile_order_launch(const int32_t* gstart, const int32_t* gend, int rows, int32_t* order,
+                                   hipStream_t stream) {
+    if (rows <= 0 || (rows + kRT - 1) / kRT > kGroupOrderTiles || !gstart || !gend || !order) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(group_tile_order, dim3(1), dim3(1024), 0, stream, gstart, gend, rows, order);
+    return hipGetLastError();
 }
 
 hipError_t group_attention_f32_x3_launch(const GroupArgs& a, int dh, hipStream_t stream) {

@@ -32,6 +32,12 @@ struct jc_ctx {
     uint64_t capture_key;
     jc::Blas* blas;          // hipBLASLt for the plain GEMMs (nullptr: the library's own kernels)
     std::vector<struct jc_prof_record>* prof;  // per-kernel timing (jc_profile), nullptr when off
+    // the group kernel's tile order (kGroupOrderTiles entries): eager calls fill `order` behind the
+    // last group kernel that read it (`order_read`, recorded on whichever stream that ran); a plan
+    // being captured fills its own buffer, `capture_order`, which the plan keeps
+    int32_t* order;
+    hipEvent_t order_read;
+    int32_t* capture_order;
 };
 
 // One timed launch: HIP events on the context's stream before and after it.
@@ -47,6 +53,7 @@ struct jc_plan {
     uint64_t key;
     std::vector<std::pair<void*, size_t>> owned;  // device buffers adopted by the plan
     hipEvent_t done = nullptr;                    // recorded behind every replay, on its stream
+    int32_t* order = nullptr;                     // the group kernels' tile order (64 KB), the plan's own
 };
 
 namespace {
@@ -226,6 +233,17 @@ int jc_init(int device, jc_ctx** out) {
         return hip_fail("jc_init: hipStreamCreate", e);
     }
     ctx->stream = ctx->own;
+    e = hipMalloc((void**)&ctx->order, sizeof(int32_t) * jc::kGroupOrderTiles);
+    if (e == hipSuccess) {
+        e = hipEventCreateWithFlags(&ctx->order_read, hipEventDisableTiming);
+        if (e != hipSuccess) (void)hipFree(ctx->order);
+    }
+    if (e != hipSuccess) {
+        (void)hipStreamDestroy(ctx->own);
+        delete ctx;
+        return hip_fail("jc_init: the group tile-order buffer", e);
+    }
+    ctx->capture_order = nullptr;
     ctx->capturing = false;
     ctx->capture_on = nullptr;
     ctx->capture_key = 0;
@@ -242,8 +260,12 @@ int jc_destroy(jc_ctx* ctx) {
         hipGraph_t g = nullptr;
         if (hipStreamEndCapture(ctx->capture_on, &g) == hipSuccess && g) (void)hipGraphDestroy(g);
         ctx->capturing = false;
+        (void)hipFree(ctx->capture_order);
     }
     (void)hipStreamSynchronize(ctx->stream);
+    (void)hipEventSynchronize(ctx->order_read);  // the last group kernel that read it, on any stream
+    (void)hipEventDestroy(ctx->order_read);
+    (void)hipFree(ctx->order);
     if (ctx->prof) {
         prof_clear(ctx);
         delete ctx->prof;
@@ -606,6 +628,28 @@ static int check_group_common(const char* W, const void* qkv, const void* out, c
     return JC_OK;
 }
 
+// The group kernel's tile order for a launch on ctx's stream (group_tile_order_launch): into the
+// captured plan's buffer, or into the context's behind the last group kernel that read it. Null
+// (the kernel's fixed order) past the buffers' capacity or with JITCAST_HIP_GROUP_ORDER=0 (read at
+// every call). Follow the group launch with group_order_done.
+static hipError_t group_order(jc_ctx* ctx, const int32_t* gs, const int32_t* ge, int rows, const int32_t** order) {
+    *order = nullptr;
+    const char* env = getenv("JITCAST_HIP_GROUP_ORDER");
+    if ((env && env[0] == '0') || (rows + 15) / 16 > jc::kGroupOrderTiles) return hipSuccess;
+    int32_t* buf = ctx->capturing ? ctx->capture_order : ctx->order;
+    if (!ctx->capturing) {
+        hipError_t e = hipStreamWaitEvent(ctx->stream, ctx->order_read, 0);
+        if (e != hipSuccess) return e;
+    }
+    hipError_t e = jc::group_tile_order_launch(gs, ge, rows, buf, ctx->stream);
+    if (e == hipSuccess) *order = buf;
+    return e;
+}
+
+static hipError_t group_order_done(jc_ctx* ctx, const int32_t* order) {
+    return order && !ctx->capturing ? hipEventRecord(ctx->order_read, ctx->stream) : hipSuccess;
+}
+
 // jc_c2_group_attention after use(); x3 as for c2_time.
 static int c2_group(jc_ctx* ctx, const char* W, const void* qkv, void* out, const int32_t* live,
                     const int32_t* group_start, const int32_t* group_end, int rows, int n, int heads, int dh, int inner,
@@ -627,8 +671,11 @@ static int c2_group(jc_ctx* ctx, const char* W, const void* qkv, void* out, cons
     a.enc = n;
     a.qscale = 1.4426950408889634f;  // unscaled scores, exp via exp2
     ProfScope ps(ctx, x3 ? "c2 group_attention (split out)" : dtype == JC_F32 ? "c2 group_attention_f32" : "c2 group_attention_lp");
-    hipError_t e = x3 ? jc::group_attention_f32_x3_launch(a, dh, ctx->stream)
-                      : jc::group_attention_launch(a, dh, false, dtype, ctx->stream);
+    hipError_t e = group_order(ctx, group_start, group_end, rows, &a.order);
+    if (e == hipSuccess)
+        e = x3 ? jc::group_attention_f32_x3_launch(a, dh, ctx->stream)
+               : jc::group_attention_launch(a, dh, false, dtype, ctx->stream);
+    if (e == hipSuccess) e = group_order_done(ctx, a.order);
     return e == hipSuccess ? JC_OK : hip_fail(W, e);
 }
 
@@ -667,7 +714,9 @@ int jc_ts_variate_attention(jc_ctx* ctx, const void* qkv, void* out, const int32
     a.covariates = covariates;
     a.qscale = (float)(1.4426950408889634 / std::sqrt((double)dh));
     ProfScope ps(ctx, dtype == JC_F32 ? "ts variate_attention_f32" : "ts variate_attention_lp");
-    hipError_t e = jc::group_attention_launch(a, dh, true, dtype, ctx->stream);
+    hipError_t e = group_order(ctx, group_start, group_end, rows, &a.order);
+    if (e == hipSuccess) e = jc::group_attention_launch(a, dh, true, dtype, ctx->stream);
+    if (e == hipSuccess) e = group_order_done(ctx, a.order);
     return e == hipSuccess ? JC_OK : hip_fail(W, e);
 }
 
@@ -680,8 +729,15 @@ int jc_plan_begin(jc_ctx* ctx, uint64_t shape_key) {
     if (ctx->capturing) return fail(JC_ESTATE, "%s: a plan is already being captured", W);
     if (ctx->stream == nullptr)
         return fail(JC_ESTATE, "%s: the null stream cannot be captured (jc_set_stream a created stream)", W);
-    hipError_t e = hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal);
-    if (e != hipSuccess) return hip_fail(W, e);
+    int32_t* order = nullptr;  // the plan's own tile-order buffer, so replays on any stream share nothing
+    hipError_t e = hipMalloc((void**)&order, sizeof(int32_t) * jc::kGroupOrderTiles);
+    if (e != hipSuccess) return hip_fail("jc_plan_begin: the group tile-order buffer", e);
+    e = hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal);
+    if (e != hipSuccess) {
+        (void)hipFree(order);
+        return hip_fail(W, e);
+    }
+    ctx->capture_order = order;
     ctx->capturing = true;
     ctx->capture_on = ctx->stream;
     ctx->capture_key = shape_key;
@@ -696,24 +752,30 @@ int jc_plan_end(jc_ctx* ctx, jc_plan** out) {
     if (rc) return rc;
     if (!ctx->capturing) return fail(JC_ESTATE, "%s: no plan is being captured", W);
     ctx->capturing = false;
+    int32_t* order = ctx->capture_order;
+    ctx->capture_order = nullptr;
     hipGraph_t graph = nullptr;
     hipError_t e = hipStreamEndCapture(ctx->capture_on, &graph);
     if (e != hipSuccess) {
         if (graph) (void)hipGraphDestroy(graph);
+        (void)hipFree(order);
         return hip_fail(W, e);
     }
     hipGraphExec_t exec = nullptr;
     e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
     if (e != hipSuccess) {
         (void)hipGraphDestroy(graph);
+        (void)hipFree(order);
         return hip_fail("jc_plan_end: hipGraphInstantiate", e);
     }
     jc_plan* plan = new (std::nothrow) jc_plan();
     if (!plan) {
         (void)hipGraphExecDestroy(exec);
         (void)hipGraphDestroy(graph);
+        (void)hipFree(order);
         return fail(JC_ENOMEM, "%s: out of host memory", W);
     }
+    plan->order = order;
     plan->ctx = ctx;
     plan->graph = graph;
     plan->exec = exec;
@@ -722,6 +784,7 @@ int jc_plan_end(jc_ctx* ctx, jc_plan** out) {
     if (e != hipSuccess) {
         (void)hipGraphExecDestroy(exec);
         (void)hipGraphDestroy(graph);
+        (void)hipFree(order);
         delete plan;
         return hip_fail("jc_plan_end: hipEventCreateWithFlags", e);
     }
@@ -783,6 +846,8 @@ int jc_plan_destroy(jc_plan* plan) {
         e = hipFree(b.first);
         if (e != hipSuccess && rc == JC_OK) rc = hip_fail("jc_plan_destroy: hipFree", e);
     }
+    e = hipFree(plan->order);
+    if (e != hipSuccess && rc == JC_OK) rc = hip_fail("jc_plan_destroy: hipFree", e);
     delete plan;
     return rc;
 }

@@ -44,7 +44,17 @@ struct GroupArgs {
     float qscale;           // score scale times log2(e), folded into q
     int rtiles;             // 16-row tiles, set by the launcher
     int hsplit;             // head ranges per (tile, slot), one wave each; set by the launcher
+    const int32_t* order;   // [rtiles] the tiles by descending work (group_tile_order_launch), or null
 };
+
+// Capacity, in 16-row tiles, of the buffers group_tile_order_launch fills.
+constexpr int kGroupOrderTiles = 16384;
+
+// The order in which the group kernel dispatches its tiles: by descending work, (16-row key tiles)^2
+// summed over the groups starting in the tile (bucketed), so the launch ends on light waves. One
+// workgroup; order gets the ceil(rows / 16) tile indices (rows <= 16 * kGroupOrderTiles).
+hipError_t group_tile_order_launch(const int32_t* gstart, const int32_t* gend, int rows, int32_t* order,
+                                   hipStream_t stream);
 
 // Chronos-2 group attention (ts = false) or Timestral variate attention (ts = true); a.rtiles is
 // set by the launcher. dh a multiple of 8, at most 128 (64 for Chronos-2). dtype (0 fp32, 1 bf16,

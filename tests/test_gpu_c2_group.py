@@ -148,3 +148,18 @@ def test_fp32_values_beyond_fp16_range(gpu, oracle, part, scale):
     assert oracle.rel_max_error(got, exp) <= TOL_F32
     other = np.repeat(group != group[20], n)  # token rows of the groups without row 20
     assert oracle.rel_max_error(got[other], exp[other]) <= TOL_F32
+
+
+def test_tile_order_changes_nothing(gpu, monkeypatch):
+    """The kernel dispatches its tiles heaviest first (an order a prep kernel sorts from the group
+    bounds); JITCAST_HIP_GROUP_ORDER=0 keeps the fixed order. Which block runs a tile changes
+    nothing in its results: bit-equal outputs, on groups of 1..64 rows and on one of 300 rows."""
+    rows, n, heads, dh, inner = 700, 3, 12, 64, 768
+    qkv = cases.qkv(51, rows * n, inner)
+    live = cases.random_live(51, rows, n, 0.9)
+    group = np.r_[cases.group_sizes(51, rows - 300, 1, 64), np.full(300, 10 ** 6, np.int32)]
+    got = {}
+    for mode in ("0", "1"):
+        monkeypatch.setenv("JITCAST_HIP_GROUP_ORDER", mode)
+        got[mode] = _run(qkv, live, group, rows, n, heads, dh, inner)
+    np.testing.assert_array_equal(got["0"], got["1"])
