@@ -51,7 +51,8 @@ typedef struct jc_plan jc_plan;
 
 /* ---- runtime (replaces TornadoVM device selection and buffers: J/tornado/Devices.java:44-73) ---- */
 
-/* Makes `device` current and creates the context's stream (default priority). */
+/* Makes `device` current and creates the context's stream (default priority) and its 64 KB buffer
+ * for the group kernels' tile order (jc_c2_group_attention). */
 int jc_init(int device, jc_ctx **ctx);
 /* Destroys the context (idempotent on NULL). */
 int jc_destroy(jc_ctx *ctx);
@@ -100,6 +101,8 @@ int jc_version(void);
  * jc_plan_launch, as the reference uploads them before each execution.
  */
 int jc_plan_begin(jc_ctx *ctx, uint64_t shape_key);
+/* (jc_plan_begin also allocates the plan's own 64 KB tile-order buffer, freed with the plan and not
+ * counted by jc_plan_device_bytes.) */
 /* Ends the capture and instantiates the plan; on error no plan is made and capture has ended. */
 int jc_plan_end(jc_ctx *ctx, jc_plan **plan);
 /* Replays the plan on the context's current stream (asynchronous; jc_sync waits). */
@@ -174,6 +177,10 @@ int jc_c2_time_attention(jc_ctx *ctx, const void *qkv, void *out, const int32_t 
  *   dh           a multiple of 8, at most 64 (the reference takes multiples of 16)
  *   dtype        the storage type of qkv and out: JC_F32, or JC_BF16 / JC_F16 (values widened to
  *                fp32 at load, scores, softmax and accumulation in fp32, out rounded once)
+ * With JC_F32 the QK^T and PV products run as three fp16 MFMA products each (v = hi + lo), within
+ * about 2^-20 of the fp32 product; a wave that meets a value beyond fp16's range runs on fp32 MFMA.
+ * A one-workgroup kernel first sorts the 16-row tiles by work (into the context's buffer, or the
+ * plan's while capturing), so the launch dispatches the heaviest first.
  */
 int jc_c2_group_attention(jc_ctx *ctx, const void *qkv, void *out, const int32_t *live, const int32_t *group_start,
                           const int32_t *group_end, int rows, int n, int heads, int dh, int inner, int dtype);

@@ -630,13 +630,14 @@ static int check_group_common(const char* W, const void* qkv, const void* out, c
 
 // The group kernel's tile order for a launch on ctx's stream (group_tile_order_launch): into the
 // captured plan's buffer, or into the context's behind the last group kernel that read it. Null
-// (the kernel's fixed order) past the buffers' capacity or with JITCAST_HIP_GROUP_ORDER=0 (read at
-// every call). Follow the group launch with group_order_done.
+// (the kernel's fixed order) without a buffer, past its capacity or with JITCAST_HIP_GROUP_ORDER=0
+// (read at every call). Follow the group launch with group_order_done.
 static hipError_t group_order(jc_ctx* ctx, const int32_t* gs, const int32_t* ge, int rows, const int32_t** order) {
     *order = nullptr;
     const char* env = getenv("JITCAST_HIP_GROUP_ORDER");
     if ((env && env[0] == '0') || (rows + 15) / 16 > jc::kGroupOrderTiles) return hipSuccess;
     int32_t* buf = ctx->capturing ? ctx->capture_order : ctx->order;
+    if (!buf) return hipSuccess;
     if (!ctx->capturing) {
         hipError_t e = hipStreamWaitEvent(ctx->stream, ctx->order_read, 0);
         if (e != hipSuccess) return e;
@@ -1023,6 +1024,10 @@ int jc_c2_layer_static(jc_ctx* ctx, float* x, const jc_c2_layer_weights* w, cons
     // on a copy of the context without hipBLASLt, which leaves the caller's context untouched
     jc_ctx own = *ctx;
     own.blas = nullptr;
+    // and the group kernel in its fixed order: its tile order would be device memory beyond the
+    // static scratch
+    own.order = nullptr;
+    own.capture_order = nullptr;
     return c2_layer(&own, W, x, w, live, table, group_start, group_end, ws, rows, n, d, heads, dh, dff, eps, dtype);
 }
 
