@@ -639,7 +639,13 @@ static hipError_t group_order(jc_ctx* ctx, const int32_t* gs, const int32_t* ge,
     int32_t* buf = ctx->capturing ? ctx->capture_order : ctx->order;
     if (!buf) return hipSuccess;
     if (!ctx->capturing) {
-        hipError_t e = hipStreamWaitEvent(ctx->stream, ctx->order_read, 0);
+        // a capture the caller began on this stream: the context's buffer and its event are not
+        // the graph's, so the kernel keeps its fixed order there
+        hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+        hipError_t e = hipStreamIsCapturing(ctx->stream, &st);
+        if (e != hipSuccess) return e;
+        if (st != hipStreamCaptureStatusNone) return hipSuccess;
+        e = hipStreamWaitEvent(ctx->stream, ctx->order_read, 0);
         if (e != hipSuccess) return e;
     }
     hipError_t e = jc::group_tile_order_launch(gs, ge, rows, buf, ctx->stream);

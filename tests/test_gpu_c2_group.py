@@ -163,3 +163,35 @@ def test_tile_order_changes_nothing(gpu, monkeypatch):
         monkeypatch.setenv("JITCAST_HIP_GROUP_ORDER", mode)
         got[mode] = _run(qkv, live, group, rows, n, heads, dh, inner)
     np.testing.assert_array_equal(got["0"], got["1"])
+
+
+def test_group_attention_under_a_callers_capture(gpu):
+    """A caller's own capture (torch.cuda.graph) of jc_c2_group_attention. The library sees the
+    stream capturing and keeps the kernel's fixed order (the context's tile-order buffer belongs to
+    eager calls). Every replay, with eager calls and a fill between them, equals the eager result
+    bit for bit."""
+    rows, n, heads, dh, inner = 200, 3, 2, 64, 128
+    dev = torch.device("cuda:0")
+    qkv = torch.from_numpy(cases.qkv(53, rows * n, inner)).to(dev)
+    live = torch.from_numpy(np.ascontiguousarray(cases.random_live(53, rows, n, 0.9).reshape(-1))).to(dev)
+    s, e = chronos2.group_bounds(cases.group_sizes(53, rows, 1, 40))
+    s, e = torch.from_numpy(s).to(dev), torch.from_numpy(e).to(dev)
+
+    def call(o):
+        chronos2.group_attention(qkv, o, live, s, e, rows, n, heads, dh, inner)
+
+    eager = torch.zeros(rows * n, inner, device=dev)
+    call(eager)
+    torch.cuda.synchronize()
+    out = torch.zeros_like(eager)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        call(out)
+    other = torch.zeros_like(eager)
+    for _ in range(3):
+        out.zero_()
+        call(other)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+        assert torch.equal(other, eager)
