@@ -175,10 +175,12 @@ int jc_c2_time_attention(jc_ctx *ctx, const void *qkv, void *out, const int32_t 
  *   qkv, out     device, as jc_c2_time_attention (the group sublayer's own projection)
  *   group_start  device int32 [rows]; group_end device int32 [rows] (jc_c2_group_bounds)
  *   dh           a multiple of 8, at most 64 (the reference takes multiples of 16)
- *   dtype        the storage type of qkv and out: JC_F32, or JC_BF16 / JC_F16 (values widened to
- *                fp32 at load, scores, softmax and accumulation in fp32, out rounded once)
+ *   dtype        the storage type of qkv and out: JC_F32, or JC_BF16 / JC_F16 (scores, softmax and
+ *                accumulation in fp32, out rounded once)
  * With JC_F32 the QK^T and PV products run as three fp16 MFMA products each (v = hi + lo), within
  * about 2^-20 of the fp32 product; a wave that meets a value beyond fp16's range runs on fp32 MFMA.
+ * With JC_BF16 / JC_F16, K and Q enter the MFMA of their type as stored (exact products), and P as a
+ * hi + lo pair of the type against V as stored.
  * A one-workgroup kernel first sorts the 16-row tiles by work (into the context's buffer, or the
  * plan's while capturing), so the launch dispatches the heaviest first.
  */

@@ -14,7 +14,9 @@
 // reads only known rows; a row always reads itself. The optional sigmoid gate is fused.
 //
 // Storage types: q|k|v, the gate and out are fp32, or (T = bf16 / fp16, the layers' FP16 GEMM mode)
-// 16-bit values widened to fp32 at load and rounded once at the store; scores, softmax and
+// 16-bit values rounded once at the store. The products: fp32 values as fp16 pairs (three fp16 MFMA
+// products per product, fp32 MFMA for values beyond fp16's range), 16-bit values as stored (exact
+// products on the MFMA of their type, P as a hi + lo pair of the type); scores, softmax and
 // accumulation are fp32 either way.
 //
 // The stage reads q|k|v once and writes out once, about 10 flop per byte: it is HBM-bound, so the
@@ -46,6 +48,30 @@ namespace jc {
 namespace {
 
 constexpr int kRT = 16;  // rows per tile (queries and keys)
+constexpr int kModeF32 = 0, kModeSplit = 1, kModeNative = 2;  // the job stream's MFMA forms
+
+// v_mfma_f32_16x16x16 of the storage type T (bf16 or fp16): A lane i+16kk = A[i][4kk..4kk+3], B lane
+// j+16kk = B[4kk..4kk+3][j], 4 values of T per operand
+template <typename T>
+__device__ __forceinline__ floatx4 mfma16(lp::u32x2 a, lp::u32x2 b, floatx4 c) {
+    typedef short s4 __attribute__((ext_vector_type(4)));
+    if constexpr (std::is_same_v<T, __bf16>) {
+        return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s4, a), __builtin_bit_cast(s4, b), c, 0, 0, 0);
+    } else {
+        return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(halfx4, a), __builtin_bit_cast(halfx4, b), c, 0, 0,
+                                                     0);
+    }
+}
+
+// p = hi + lo in T, both rounded to nearest: within 2^-16 |p| (bf16) or 2^-22 |p| + 2^-25 (fp16)
+template <typename T>
+__device__ __forceinline__ void split_lp(floatx4 p, lp::u32x2& hi, lp::u32x2& lo) {
+    typedef T t4 __attribute__((ext_vector_type(4)));
+    const t4 h = __builtin_convertvector(p, t4);
+    const t4 l = __builtin_convertvector(p - __builtin_convertvector(h, floatx4), t4);
+    hi = __builtin_bit_cast(lp::u32x2, h);
+    lo = __builtin_bit_cast(lp::u32x2, l);
+}
 
 // four consecutive storage values as fp32 (one 16- or 8-byte load), and back
 template <typename T>
@@ -211,7 +237,15 @@ __global__ __launch_bounds__(kWave) void group_attention_f32(const GroupArgs a, 
         float v[kM][4];
         int valid, role;
     };
-    auto load_kv = [&](const Job& jb, Kv& d) {
+    // (bf16 / fp16 storage, NATIVE below) the same operands as stored: K's 4 dims per m and, per m,
+    // V[key 4g + c][16m + j] for c = 0..3 packed as one 4-value operand
+    struct KvN {
+        lp::u32x2 k[kM];
+        lp::u32x2 v[kM];
+        int valid, role;
+    };
+    auto load_kv = [&](const Job& jb, auto& d) {
+        constexpr bool kRaw = std::is_same_v<std::decay_t<decltype(d)>, KvN>;
         const int kbase = jb.gs + kRT * jb.kt;
         const int krow = min(kbase + j, jb.ge - 1);
         const T* kp = qkv + ((size_t)krow * tok_n + t) * stride + inner + jb.h * dh + 4 * g;
@@ -223,31 +257,57 @@ __global__ __launch_bounds__(kWave) void group_attention_f32(const GroupArgs a, 
             d.valid = in_group ? a.valid[(size_t)krow * tok_n + t] : 0;
             d.role = 0;
         }
+        if constexpr (kRaw) {
+            uint16_t vb[kM][4];
 #pragma unroll
-        for (int m = 0; m < kM; m++)
-            d.k[m] = (EXACT || 16 * m + 4 * g < dh) ? load4(kp + 16 * m) : floatx4{0.f, 0.f, 0.f, 0.f};
+            for (int m = 0; m < kM; m++)
+                d.k[m] = (EXACT || 16 * m + 4 * g < dh) ? *reinterpret_cast<const lp::u32x2*>(kp + 16 * m) : lp::u32x2{0u, 0u};
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const int vrow = min(kbase + 4 * g + c, jb.ge - 1);
-            const T* vp = qkv + ((size_t)vrow * tok_n + t) * stride + 2 * inner + jb.h * dh + j;
+            for (int c = 0; c < 4; c++) {
+                const int vrow = min(kbase + 4 * g + c, jb.ge - 1);
+                const uint16_t* vp = reinterpret_cast<const uint16_t*>(qkv + ((size_t)vrow * tok_n + t) * stride +
+                                                                      2 * inner + jb.h * dh + j);
 #pragma unroll
-            for (int m = 0; m < kM; m++) d.v[m][c] = (EXACT || 16 * m + j < dh) ? (float)vp[16 * m] : 0.f;
+                for (int m = 0; m < kM; m++) vb[m][c] = (EXACT || 16 * m + j < dh) ? vp[16 * m] : (uint16_t)0;
+            }
+#pragma unroll
+            for (int m = 0; m < kM; m++)
+                d.v[m] = lp::u32x2{vb[m][0] | ((uint32_t)vb[m][1] << 16), vb[m][2] | ((uint32_t)vb[m][3] << 16)};
+        } else {
+#pragma unroll
+            for (int m = 0; m < kM; m++)
+                d.k[m] = (EXACT || 16 * m + 4 * g < dh) ? load4(kp + 16 * m) : floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const int vrow = min(kbase + 4 * g + c, jb.ge - 1);
+                const T* vp = qkv + ((size_t)vrow * tok_n + t) * stride + 2 * inner + jb.h * dh + j;
+#pragma unroll
+                for (int m = 0; m < kM; m++) d.v[m][c] = (EXACT || 16 * m + j < dh) ? (float)vp[16 * m] : 0.f;
+            }
         }
     };
 
-    // The job stream. SPLIT (fp32 storage): QK^T and PV as three fp16 MFMA products each
-    // (split_f16), a quarter of the fp32 MFMA cycles. It gives up, returning false, at the first
-    // query, key or value outside fp16's range (or infinite); the wave then runs its whole stream
-    // again on fp32 MFMA, which writes every output of the wave anew.
-    auto stream = [&](auto split_tag) -> bool {
-        constexpr bool SPLIT = decltype(split_tag)::value;
+    // The job stream, in one of three modes:
+    //   kModeF32    v_mfma_f32_16x16x4f32 on fp32 values (widened from the storage type);
+    //   kModeSplit  fp32 storage: QK^T and PV as three fp16 MFMA products each (split_f16), a quarter
+    //               of the fp32 MFMA cycles. It gives up, returning false, at the first query, key or
+    //               value outside fp16's range (or infinite); the wave then runs its whole stream
+    //               again in kModeF32, which writes every output of the wave anew;
+    //   kModeNative bf16 / fp16 storage: K and Q as stored on the 16x16x16 MFMA of their type (exact
+    //               products; qscale applied to the fp32 scores), and P as a pair of the storage
+    //               type, hi + lo, against V as stored: two products per value tile.
+    auto stream = [&](auto mode_tag) -> bool {
+        constexpr int MODE = decltype(mode_tag)::value;
+        constexpr bool SPLIT = MODE == kModeSplit, NATIVE = MODE == kModeNative;
         Job cur = first_of(starts);
-        Kv dc, dn;
+        std::conditional_t<NATIVE, KvN, Kv> dc, dn;
         load_kv(cur, dc);
 
-        // resident query tiles (B operand), scaled by qscale: fp32, or (SPLIT) their fp16 pairs
-        float qreg[SPLIT ? 1 : kQT][4 * kM];
+        // resident query tiles (B operand): fp32 scaled by qscale, (SPLIT) their fp16 pairs, or
+        // (NATIVE) the stored values, unscaled
+        float qreg[MODE == kModeF32 ? kQT : 1][4 * kM];
         halfx4 qhi[SPLIT ? kQT : 1][kM], qlo[SPLIT ? kQT : 1][kM];
+        lp::u32x2 qn[NATIVE ? kQT : 1][kM];
         floatx4 o_acc[kQT][kM];
         float m_run[kQT], l_run[kQT];
         int q_role[kQT];
@@ -274,6 +334,11 @@ __global__ __launch_bounds__(kWave) void group_attention_f32(const GroupArgs a, 
                         const T* qp = qkv + ((size_t)qrow * tok_n + t) * stride + cur.h * dh + 4 * g;
 #pragma unroll
                         for (int m = 0; m < kM; m++) {
+                            if constexpr (NATIVE) {
+                                qn[qi][m] = (EXACT || 16 * m + 4 * g < dh) ? *reinterpret_cast<const lp::u32x2*>(qp + 16 * m)
+                                                                          : lp::u32x2{0u, 0u};
+                                continue;
+                            }
                             const floatx4 x = ((EXACT || 16 * m + 4 * g < dh) ? load4(qp + 16 * m)
                                                                              : floatx4{0.f, 0.f, 0.f, 0.f}) *
                                               a.qscale;
@@ -371,6 +436,30 @@ __global__ __launch_bounds__(kWave) void group_attention_f32(const GroupArgs a, 
                         }
                     }
                 }
+            } else if constexpr (NATIVE) {
+#pragma unroll
+                for (int qi = 0; qi < kQT; qi++) {
+                    if (qi < nq) {
+                        floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                        for (int m = 0; m < kM; m++) {
+                            if (EXACT || 16 * m < dh) s = mfma16<T>(dc.k[m], qn[qi][m], s);
+                        }
+                        s *= a.qscale;
+                        const float alpha = softmax(qi, s);
+                        // O^T += V^T P_hi + V^T P_lo, P = P_hi + P_lo in the storage type (P in [0, 1])
+                        lp::u32x2 phi, plo;
+                        split_lp<T>(s, phi, plo);
+#pragma unroll
+                        for (int m = 0; m < kM; m++) {
+                            if (EXACT || 16 * m < dh) {
+                                floatx4 acc = o_acc[qi][m] * alpha;
+                                acc = mfma16<T>(dc.v[m], phi, acc);
+                                o_acc[qi][m] = mfma16<T>(dc.v[m], plo, acc);
+                            }
+                        }
+                    }
+                }
             } else {
 #pragma unroll
                 for (int qi = 0; qi < kQT; qi++) {
@@ -437,7 +526,11 @@ __global__ __launch_bounds__(kWave) void group_attention_f32(const GroupArgs a, 
         }
         return true;
     };
-    if (!stream(std::bool_constant<std::is_same_v<T, float>>{})) stream(std::false_type{});
+    if constexpr (std::is_same_v<T, float>) {
+        if (!stream(std::integral_constant<int, kModeSplit>{})) stream(std::integral_constant<int, kModeF32>{});
+    } else {
+        stream(std::integral_constant<int, kModeNative>{});
+    }
 }
 
 }  // namespace

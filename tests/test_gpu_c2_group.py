@@ -1,5 +1,6 @@
 """GPU parity of Chronos-2 group attention against the C oracle (through the C ABI). Bars: max
-relative error <= 1e-4 (fp32). bf16 / fp16 storage (fp32 arithmetic, the output rounded once): against
+relative error <= 1e-4 (fp32). bf16 / fp16 storage (exact 16-bit products, fp32 softmax and sums, the
+output rounded once): against
 the oracle on the same rounded inputs within 2^-8 (bf16) / 2^-11 (fp16), the output's own rounding
 with room to spare, and against the oracle on the unrounded fp32 inputs within 2e-2."""
 import numpy as np
