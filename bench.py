@@ -160,6 +160,13 @@ def group_attention_line(steps: int, warmup: int, cpu: bool = True) -> dict:
     nbytes = case.algorithmic_bytes()
     gbs = nbytes / (ms * 1e-3) / 1e9
     log(f"group attention: {ms:.4f} ms, {gbs:.0f} GB/s algorithmic ({100 * gbs / PEAK_HBM_GBS:.1f}% of HBM)")
+    # the same launches with fp32 storage on fp32 MFMA throughout instead of three-term fp16 products
+    os.environ["JITCAST_HIP_GROUP_F32MMA"] = "1"
+    try:
+        ms32 = time_launches(fn, steps, warmup)
+    finally:
+        del os.environ["JITCAST_HIP_GROUP_F32MMA"]
+    log(f"group attention on fp32 MFMA: {ms32:.4f} ms ({100 * nbytes / (ms32 * 1e-3) / 1e9 / PEAK_HBM_GBS:.1f}% of HBM)")
     res = {
         "workload": "config 2: fp32 Chronos-2 group attention, 4096 rows x 129 slots, 12x64, groups U{1..64}",
         "kernel": "jc::group_attention_f32<float, 64, false, true, false>",
@@ -170,6 +177,8 @@ def group_attention_line(steps: int, warmup: int, cpu: bool = True) -> dict:
                      "frac": round(gbs / PEAK_HBM_GBS, 4), **from_profile("c2_group_attention_f32_config2", gbs / PEAK_HBM_GBS, ms)},
         "bytes_per_launch": nbytes,
         "tflops": round(case.flops() / (ms * 1e-3) / 1e12, 2),
+        "products": "three-term fp16 MFMA products (v = hi + lo), fp32 softmax and accumulation",
+        "fp32_mfma_launch_ms": round(ms32, 5),
     }
     if cpu:
         res["cpu_baseline"] = group_cpu_baseline(case, cpu_threads())

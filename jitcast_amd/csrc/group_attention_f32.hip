@@ -527,7 +527,8 @@ __global__ __launch_bounds__(kWave) void group_attention_f32(const GroupArgs a, 
         return true;
     };
     if constexpr (std::is_same_v<T, float>) {
-        if (!stream(std::integral_constant<int, kModeSplit>{})) stream(std::integral_constant<int, kModeF32>{});
+        if (a.f32_mfma || !stream(std::integral_constant<int, kModeSplit>{}))
+            stream(std::integral_constant<int, kModeF32>{});
     } else {
         stream(std::integral_constant<int, kModeNative>{});
     }
@@ -544,6 +545,13 @@ static int group_head_split() {
     const char* e = getenv("JITCAST_HIP_GROUP_SPLIT");
     const int v = e ? atoi(e) : 0;
     return v >= 1 && v <= 16 ? v : 4;
+}
+
+// JITCAST_HIP_GROUP_F32MMA=1 runs fp32 storage on fp32 MFMA throughout (the three-term fp16 products
+// are the default); read at every launch.
+static int group_f32_mfma() {
+    const char* e = getenv("JITCAST_HIP_GROUP_F32MMA");
+    return e && e[0] == '1' ? 1 : 0;
 }
 
 constexpr int kOrderBuckets = 64;
@@ -596,6 +604,7 @@ template <typename T, int DHP, bool TS, bool EXACT, bool X3 = false>
 static hipError_t launch_group(GroupArgs a, int dh, hipStream_t stream) {
     a.rtiles = (a.rows + kRT - 1) / kRT;
     a.hsplit = std::min(group_head_split(), a.heads);
+    a.f32_mfma = group_f32_mfma();
     if (a.rtiles > kGroupOrderTiles) a.order = nullptr;
     const uint64_t grid = (uint64_t)a.rtiles * a.n * a.hsplit;
     if (grid > 0xffffffffull) return hipErrorInvalidValue;

@@ -45,6 +45,7 @@ struct GroupArgs {
     int rtiles;             // 16-row tiles, set by the launcher
     int hsplit;             // head ranges per (tile, slot), one wave each; set by the launcher
     const int32_t* order;   // [rtiles] the tiles by descending work (group_tile_order_launch), or null
+    int f32_mfma;           // fp32 storage on fp32 MFMA instead of three-term fp16 products; set by the launcher
 };
 
 // Capacity, in 16-row tiles, of the buffers group_tile_order_launch fills.

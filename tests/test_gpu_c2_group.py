@@ -196,3 +196,20 @@ def test_group_attention_under_a_callers_capture(gpu):
         torch.cuda.synchronize()
         assert torch.equal(out, eager)
         assert torch.equal(other, eager)
+
+
+@pytest.mark.parametrize("rows,n,heads,dh,inner,lo,hi,p", [CASES[1], CASES[2], CASES[11], CASES[14]])
+def test_fp32_mfma_form_matches_oracle(gpu, oracle, monkeypatch, rows, n, heads, dh, inner, lo, hi, p):
+    """JITCAST_HIP_GROUP_F32MMA=1: fp32 storage on fp32 MFMA throughout, against the oracle at the fp32
+    bar, and beside the default three-term fp16 products (both within the bar of each other)."""
+    qkv = cases.qkv(41, rows * n, inner)
+    live = cases.random_live(41, rows, n, p)
+    group = cases.group_sizes(41, rows, lo, hi)
+    exp = oracle.c2_group_attention(qkv, live, group, rows, n, heads, dh, inner)[:, : heads * dh]
+    split = _run(qkv, live, group, rows, n, heads, dh, inner)[:, : heads * dh]
+    monkeypatch.setenv("JITCAST_HIP_GROUP_F32MMA", "1")
+    f32 = _run(qkv, live, group, rows, n, heads, dh, inner)[:, : heads * dh]
+    e32, es = oracle.rel_max_error(f32, exp), oracle.rel_max_error(split, exp)
+    print(f"  rel err fp32 MFMA {e32:.3e}, fp16 pairs {es:.3e}", flush=True)
+    assert e32 <= TOL_F32 and es <= TOL_F32
+    assert oracle.rel_max_error(split, f32) <= TOL_F32
