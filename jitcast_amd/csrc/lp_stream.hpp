@@ -1,7 +1,7 @@
 // Building blocks of the bf16 / fp16 time-attention kernels that stream K/V blocks through LDS
 // with direct-to-LDS loads (time_attention_lpp.hip, time_attention_lps.hip): swizzled 64-element
 // rows, the loads, waits and barriers as inline assembly, cross-lane reductions, transposing LDS
-// reads, and one query tile's online-softmax state.
+// reads, and one query tile's online-softmax state and steps.
 #pragma once
 
 #include "lp_common.hpp"
@@ -121,6 +121,86 @@ struct Tile {
     bool has_ref, any_resid;
     uint32_t qx0;
 };
+
+// The online softmax of one 32-query tile against a 32-key half block, the scores s_acc (16 per
+// lane, already relative to the tile's reference max m_mfma: the extra QK^T step) to P rounded to
+// T (two 8-value operands) and the half block's row sum lb (v_dot2 over those same values).
+// The fast path: P = exp2(S) against the current reference; true when some lane's sum leaves the
+// range it can carry (the slow path then recomputes P).
+template <typename T>
+__device__ __forceinline__ bool softmax_fast(const Tile& st, const floatx16& s_acc, typename Lp<T>::x8 (&p)[2],
+                                             float& lb) {
+    typedef typename Lp<T>::x8 x8;
+    typedef Enc<T> E;
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+        floatx4 lo, hi;
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            lo[u] = fast_exp2(s_acc[8 * c + u]);
+            hi[u] = fast_exp2(s_acc[8 * c + 4 + u]);
+        }
+        p[c] = __builtin_bit_cast(x8, narrow8<T>(lo, hi));
+    }
+    float acc = 0.f;
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+        u32x4 w = __builtin_bit_cast(u32x4, p[c]);
+#pragma unroll
+        for (int d = 0; d < 4; d++) acc = E::dot2(w[d], acc);
+    }
+    lb = pair_sum(acc);
+    const bool bad = !(lb <= kSumHi) || (!st.has_ref && !(lb >= kSumLo));
+    return (bool)__any(bad);
+}
+
+// The slow path: the exact block max, a new reference rounded to T (so the extra QK^T step encodes
+// it exactly; qx0 carries it for lanes g == 0), P against it, and the rescale of O and l.
+template <typename T>
+__device__ __forceinline__ void softmax_slow(Tile& st, const floatx16& s_acc, typename Lp<T>::x8 (&p)[2], float& lb,
+                                             int g) {
+    typedef typename Lp<T>::x8 x8;
+    typedef Enc<T> E;
+    float mx = s_acc[0];
+#pragma unroll
+    for (int rho = 1; rho < 16; rho++) mx = fmaxf(mx, s_acc[rho]);
+    mx = pair_max(mx);
+    const float s_max = st.m_mfma + mx;
+    float m_new = st.has_ref ? fmaxf(st.m_tot, s_max) : s_max;
+    const uint32_t bm = to_bits<T>(fminf(fmaxf(-m_new, -E::kMax), E::kMax));
+    const float m_enc = -from_bits<T>(bm);
+    if (fabsf(m_new) <= E::kMax) m_new = m_enc;  // keep the reference exactly encodable
+    const float shift = m_new - st.m_mfma;
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+        floatx4 lo, hi;
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            lo[u] = fast_exp2(s_acc[8 * c + u] - shift);
+            hi[u] = fast_exp2(s_acc[8 * c + 4 + u] - shift);
+        }
+        p[c] = __builtin_bit_cast(x8, narrow8<T>(lo, hi));
+    }
+    float acc = 0.f;
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+        u32x4 w = __builtin_bit_cast(u32x4, p[c]);
+#pragma unroll
+        for (int d = 0; d < 4; d++) acc = E::dot2(w[d], acc);
+    }
+    lb = pair_sum(acc);
+    if (st.has_ref) {
+        const float alpha = fast_exp2(st.m_tot - m_new);
+        st.o[0] *= alpha;
+        st.o[1] *= alpha;
+        st.l_run *= alpha;
+    }
+    st.m_tot = m_new;
+    st.m_mfma = m_enc;
+    st.resid = st.m_tot - st.m_mfma;
+    st.any_resid = __any(st.resid != 0.f);
+    st.qx0 = g == 0 ? (E::kBigQ | (bm << 16)) : 0u;
+}
 
 }  // namespace lp
 }  // namespace jc

@@ -284,71 +284,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     // the softmax slow path: the exact block max, a new reference rounded to T, P recomputed, the
     // O/l rescale (a wave-uniform branch, taken when a block's sums leave the fast path's range)
     auto softmax_slow = [&](Tile& st, floatx16& s_acc, x8 (&p)[2], float& lb) __attribute__((always_inline)) {
-        float mx = s_acc[0];
-#pragma unroll
-        for (int rho = 1; rho < 16; rho++) mx = fmaxf(mx, s_acc[rho]);
-        mx = pair_max(mx);
-        const float s_max = st.m_mfma + mx;
-        float m_new = st.has_ref ? fmaxf(st.m_tot, s_max) : s_max;
-        const uint32_t bm = to_bits<T>(fminf(fmaxf(-m_new, -E::kMax), E::kMax));
-        const float m_enc = -from_bits<T>(bm);
-        if (fabsf(m_new) <= E::kMax) m_new = m_enc;  // keep the reference exactly encodable
-        const float shift = m_new - st.m_mfma;
-#pragma unroll
-        for (int c = 0; c < 2; c++) {
-            floatx4 lo, hi;
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
-                lo[u] = fast_exp2(s_acc[8 * c + u] - shift);
-                hi[u] = fast_exp2(s_acc[8 * c + 4 + u] - shift);
-            }
-            p[c] = __builtin_bit_cast(x8, narrow8<T>(lo, hi));
-        }
-        float acc = 0.f;
-#pragma unroll
-        for (int c = 0; c < 2; c++) {
-            u32x4 w = __builtin_bit_cast(u32x4, p[c]);
-#pragma unroll
-            for (int d = 0; d < 4; d++) acc = E::dot2(w[d], acc);
-        }
-        lb = pair_sum(acc);
-        if (st.has_ref) {
-            const float alpha = fast_exp2(st.m_tot - m_new);
-            st.o[0] *= alpha;
-            st.o[1] *= alpha;
-            st.l_run *= alpha;
-        }
-        st.m_tot = m_new;
-        st.m_mfma = m_enc;
-        st.resid = st.m_tot - st.m_mfma;
-        st.any_resid = __any(st.resid != 0.f);
-        st.qx0 = g == 0 ? (E::kBigQ | (bm << 16)) : 0u;
+        lp::softmax_slow<T>(st, s_acc, p, lb, g);
     };
 
     // The two tiles against one block. The softmax fast path assumes a reference without residual
     // (always, short of scores beyond the storage type's range); a tile carrying one takes the
     // slow path, which applies it.
     auto sm_fast = [&](Tile& st, const floatx16& s_acc, x8 (&p)[2], float& lb) __attribute__((always_inline)) {
-#pragma unroll
-        for (int c = 0; c < 2; c++) {
-            floatx4 lo, hi;
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
-                lo[u] = fast_exp2(s_acc[8 * c + u]);
-                hi[u] = fast_exp2(s_acc[8 * c + 4 + u]);
-            }
-            p[c] = __builtin_bit_cast(x8, narrow8<T>(lo, hi));
-        }
-        float acc = 0.f;
-#pragma unroll
-        for (int c = 0; c < 2; c++) {
-            u32x4 w = __builtin_bit_cast(u32x4, p[c]);
-#pragma unroll
-            for (int d = 0; d < 4; d++) acc = E::dot2(w[d], acc);
-        }
-        lb = pair_sum(acc);
-        const bool bad = !(lb <= kSumHi) || (!st.has_ref && !(lb >= kSumLo));
-        return (bool)__any(bad);
+        return lp::softmax_fast<T>(st, s_acc, p, lb);
     };
     auto compute = [&](int slot, uint64_t kmask) __attribute__((always_inline)) {
         const uint16_t* kb = lds.kv[slot][0];

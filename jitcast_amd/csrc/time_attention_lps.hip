@@ -258,69 +258,12 @@ time_attention_lps(const TimeArgs a, int items, int groups) {
     // the softmax slow path: the exact block max, a new reference rounded to T, P recomputed, the
     // O/l rescale (a wave-uniform branch, taken when a block's sums leave the fast path's range)
     auto softmax_slow = [&](floatx16& s_acc, x8 (&p)[2], float& lb) __attribute__((always_inline)) {
-        float mx = s_acc[0];
-#pragma unroll
-        for (int rho = 1; rho < 16; rho++) mx = fmaxf(mx, s_acc[rho]);
-        mx = pair_max(mx);
-        const float s_max = tl.m_mfma + mx;
-        float m_new = tl.has_ref ? fmaxf(tl.m_tot, s_max) : s_max;
-        const uint32_t bm = to_bits<T>(fminf(fmaxf(-m_new, -E::kMax), E::kMax));
-        const float m_enc = -from_bits<T>(bm);
-        if (fabsf(m_new) <= E::kMax) m_new = m_enc;  // keep the reference exactly encodable
-        const float shift = m_new - tl.m_mfma;
-#pragma unroll
-        for (int c = 0; c < 2; c++) {
-            floatx4 lo, hi;
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
-                lo[u] = fast_exp2(s_acc[8 * c + u] - shift);
-                hi[u] = fast_exp2(s_acc[8 * c + 4 + u] - shift);
-            }
-            p[c] = __builtin_bit_cast(x8, narrow8<T>(lo, hi));
-        }
-        float acc = 0.f;
-#pragma unroll
-        for (int c = 0; c < 2; c++) {
-            u32x4 w = __builtin_bit_cast(u32x4, p[c]);
-#pragma unroll
-            for (int d = 0; d < 4; d++) acc = E::dot2(w[d], acc);
-        }
-        lb = pair_sum(acc);
-        if (tl.has_ref) {
-            const float alpha = fast_exp2(tl.m_tot - m_new);
-            tl.o[0] *= alpha;
-            tl.o[1] *= alpha;
-            tl.l_run *= alpha;
-        }
-        tl.m_tot = m_new;
-        tl.m_mfma = m_enc;
-        tl.resid = tl.m_tot - tl.m_mfma;
-        tl.any_resid = __any(tl.resid != 0.f);
-        tl.qx0 = g == 0 ? (E::kBigQ | (bm << 16)) : 0u;
+        lp::softmax_slow<T>(tl, s_acc, p, lb, g);
     };
     // the fast path: P = exp2(S) against the current reference; true when a block's sum leaves
     // the range it can carry (the slow path then recomputes it)
     auto sm_fast = [&](const floatx16& s_acc, x8 (&p)[2], float& lb) __attribute__((always_inline)) {
-#pragma unroll
-        for (int c = 0; c < 2; c++) {
-            floatx4 lo, hi;
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
-                lo[u] = fast_exp2(s_acc[8 * c + u]);
-                hi[u] = fast_exp2(s_acc[8 * c + 4 + u]);
-            }
-            p[c] = __builtin_bit_cast(x8, narrow8<T>(lo, hi));
-        }
-        float acc = 0.f;
-#pragma unroll
-        for (int c = 0; c < 2; c++) {
-            u32x4 w = __builtin_bit_cast(u32x4, p[c]);
-#pragma unroll
-            for (int d = 0; d < 4; d++) acc = E::dot2(w[d], acc);
-        }
-        lb = pair_sum(acc);
-        const bool bad = !(lb <= kSumHi) || (!tl.has_ref && !(lb >= kSumLo));
-        return (bool)__any(bad);
+        return lp::softmax_fast<T>(tl, s_acc, p, lb);
     };
     // the wave's tile against element e's block, per 32-key half: QK^T (4 steps and the mask /
     // reference step), the softmax, PV from transposing reads of V; halves without a live key are
