@@ -213,3 +213,19 @@ def test_fp32_mfma_form_matches_oracle(gpu, oracle, monkeypatch, rows, n, heads,
     print(f"  rel err fp32 MFMA {e32:.3e}, fp16 pairs {es:.3e}", flush=True)
     assert e32 <= TOL_F32 and es <= TOL_F32
     assert oracle.rel_max_error(split, f32) <= TOL_F32
+
+
+@pytest.mark.parametrize("rows", [16 * 16384, 16 * 16384 + 21])
+def test_tile_order_at_its_capacity(gpu, oracle, rows):
+    """The tile order holds 16,384 tiles (262,144 rows): at exactly that many the prep kernel sorts
+    them all (its LDS bucket array full), one tile more and the kernel keeps its fixed order. One
+    slot, one 8-wide head, groups of 1..64, against the oracle."""
+    n, heads, dh, inner = 1, 1, 8, 8
+    print(f"case rows={rows}", flush=True)
+    qkv = cases.qkv(57, rows * n, inner)
+    live = cases.random_live(57, rows, n, 0.9)
+    group = cases.group_sizes(57, rows, 1, 64)
+    got = _run(qkv, live, group, rows, n, heads, dh, inner)
+    exp = oracle.c2_group_attention(qkv, live, group, rows, n, heads, dh, inner)
+    assert np.isfinite(got).all()
+    assert oracle.rel_max_error(got, exp) <= TOL_F32
