@@ -695,7 +695,8 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (each series and each "
-              "group is independent; see DESIGN.md for how the path would shard)", file=sys.stderr)
+              "group is independent, so the path would shard by whole groups of rows, one share per GPU)",
+              file=sys.stderr)
         return 2
 
     import torch
