@@ -22,19 +22,24 @@
 // The stage reads q|k|v once and writes out once, about 10 flop per byte: it is HBM-bound, so the
 // kernel is built around the memory stream. One wave per (16-row tile, slot) owns the groups that
 // START in its tile (found by a ballot on groupStart[i] == i), so each row's q, k and v are fetched
-// from HBM once; everything lives in registers (no LDS, no barriers). The wave's work is a flat
+// from HBM once; everything lives in registers (no LDS, no barriers). A one-workgroup kernel
+// (group_tile_order) first sorts the tiles by work, and the grid dispatches the heaviest first, so
+// the launch ends on light waves. The wave's work is a flat
 // stream of jobs (group, chunk of up to 4 query tiles (2 for heads over 64 wide), head, 16-key
 // tile): the chunk's queries and output accumulators stay in registers while the group's key tiles
 // stream past, each K/V tile used by every query tile right after it lands, and the next job's K/V loads are issued before this
 // job's MFMAs (register double-buffering). The online softmax across key tiles makes any group size
 // work; a group past 64 rows re-streams its keys once per further 64-row chunk.
 //
-// Operand layouts (16x16x4 f32: A lane i+16kk = A[i][kk], B lane j+16kk = B[kk][j],
-// D lane j+16g reg r = D[4g+r][j]):
-//   S^T[key][q] = K Q^T: step s = 4m+u contracts dim 16m + 4kk + u, so each lane's K and Q come
-//                        from one 16-byte load per m and a 64-byte run per row per load.
-//   O^T[e][q] += V^T P^T: step c contracts key 4kk + c, whose P^T is S^T's reg c; V^T is loaded
-//                        per lane as V[key][e] (16 rows x 64 contiguous bytes per load).
+// Operand layouts (16x16x4 f32: A lane i+16kk = A[i][kk], B lane j+16kk = B[kk][j]; 16x16x16
+// f16 / bf16: A lane i+16kk = A[i][4kk..4kk+3], B likewise by column; D lane j+16g reg r =
+// D[4g+r][j] for both):
+//   S^T[key][q] = K Q^T: each lane holds dims 16m + 4kk .. +3 of its key and of its query (one 16-
+//                        or 8-byte load per m, a 64-byte run per row per load): 4 fp32 steps per m,
+//                        or one 16x16x16 product per m and term.
+//   O^T[e][q] += V^T P^T: keys 4kk + c (c = 0..3), whose P^T is S^T's reg c in the same lane; V^T
+//                        is loaded per lane as V[key][e] (16 rows x 64 contiguous bytes per load):
+//                        4 fp32 steps, or one 16x16x16 product per term.
 #include <algorithm>
 #include <cstdlib>
 #include <type_traits>
